@@ -1,0 +1,180 @@
+"""Benchmark of the LongSpark verify-and-refresh hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
+
+A step is one pass of the hot path over one batch of synthetic input that is
+already resident in HBM.  W untimed warm-up steps run first, then exactly K
+timed steps bracketed by ``torch.cuda.synchronize()``.  Rank 0 prints one
+JSON line with the metric (verified rows/s), the roofline of the dominant
+kernel (algorithmic bytes / its average duration, measured with HIP events
+on the stream it runs on) and a CPU baseline (the oracle's torch-CPU
+restatement of the reference path, timed on a bounded sample on this host).
+
+This build targets one GPU; ``--gpus`` above 1 exits with a message.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+V = 151936
+
+
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def time_cpu(fn, *, warmup=3, reps=20, budget_s=30.0):
+    """Median wall time (s) of ``fn`` over ``reps`` runs after ``warmup`` runs,
+    stopping early once ``budget_s`` of timed work has accumulated (>= 5 runs)."""
+    for _ in range(warmup):
+        fn()
+    times = []
+    spent = 0.0
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        dt = time.perf_counter() - t0
+        times.append(dt)
+        spent += dt
+        if spent > budget_s and len(times) >= 5:
+            break
+    return statistics.median(times), len(times)
+
+
+# --------------------------------------------------------------------------
+# workloads
+# --------------------------------------------------------------------------
+
+class GreedyVerify:
+    """Greedy chain verification, batch 128 x block 16 x vocab 151,936 bf16."""
+
+    name = "verify_greedy"
+
+    def __init__(self, dev, batch=128, width=16, vocab=V):
+        from longspark_amd import workloads
+        self.dev, self.batch, self.width, self.vocab = dev, batch, width, vocab
+        self.logits, self.cand = workloads.greedy_inputs(batch, width, vocab, seed=2024, device=dev,
+                                                         gen_device=dev)
+        self.rows = batch * width
+        # algorithmic bytes: every logit once, candidates once, outputs once
+        self.bytes = self.rows * vocab * 2 + batch * width * 4 + batch * (4 + 8)
+        self.kernel = "greedy_verify_kernel"
+
+    def step(self):
+        from longspark_amd import verify
+        return verify.verify_greedy(logits=self.logits, candidates=self.cand, width=self.width)
+
+    def config(self):
+        return {"workload": f"greedy chain verify B={self.batch} K={self.width} V={self.vocab} bf16 "
+                            "(logits N(0,3^2), drafted token +8 w.p. 0.7)",
+                "batch": self.batch, "block": self.width, "vocab": self.vocab}
+
+    def cpu_baseline(self, threads):
+        from oracle import verify as ov
+        from longspark_amd import workloads
+        b = 16
+        logits, cand = workloads.greedy_inputs(b, self.width, self.vocab, seed=7)
+        logits = logits.float()  # the reference verifier sees fp32 logits
+        cand = cand.long()
+        torch.set_num_threads(threads)
+        med, n = time_cpu(lambda: ov.accept_greedy(cand, logits, self.width))
+        return {"rows_per_s": b * self.width / med, "sample": f"B={b} x K={self.width} x V={self.vocab} "
+                f"fp32 logits, median of {n} runs", "threads": threads}
+
+
+WORKLOADS = {w.name: w for w in (GreedyVerify,)}
+DEFAULT_WORKLOAD = "verify_greedy"
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default=DEFAULT_WORKLOAD, choices=sorted(WORKLOADS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args(argv)
+    if args.gpus != 1:
+        print("bench.py: this build measures one GPU only (the hot path is per-GPU; "
+              "multi-GPU sharding is a design note, not a measured configuration)", file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        return 2
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    wl = WORKLOADS[args.workload](dev)
+    stream = torch.cuda.current_stream(dev)
+
+    for _ in range(args.warmup):
+        wl.step()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record(stream)
+    for _ in range(args.steps):
+        wl.step()
+    end.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = wall / args.steps * 1e3
+    kernel_ms = start.elapsed_time(end) / args.steps
+    value = wl.rows / (ms_per_step / 1e3)
+    achieved = wl.bytes / (kernel_ms / 1e3) / 1e9
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        ncores = len(os.sched_getaffinity(0))
+        allc = wl.cpu_baseline(ncores)
+        four = wl.cpu_baseline(4)
+        cpu = {"value": allc["rows_per_s"], "unit": "rows/s", "cores": ncores, "kind": "port",
+               "sample": allc["sample"], "cpu_model": _cpu_model(),
+               "value_4_threads": four["rows_per_s"]}
+
+    line = {
+        "metric": "verified rows/sec at Bx16x151936 bf16",
+        "value": value,
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": wl.config(),
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel": wl.kernel,
+                     "kernel_avg_us": kernel_ms * 1e3, "algorithmic_bytes": wl.bytes},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

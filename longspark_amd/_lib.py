@@ -1,0 +1,129 @@
+"""ctypes binding of ``liblongspark_amd.so`` (the C ABI in ``include/longspark_amd.h``).
+
+The library is loaded from the package directory; there is no fallback: if it
+is missing, importing this module raises with the command that builds it.
+Status codes returned by the C ABI are mapped to the exception types the
+reference wrappers raise before launching (``ValueError`` for shape, dtype,
+alignment, workspace and value errors; ``RuntimeError`` for launch errors).
+"""
+
+from __future__ import annotations
+
+import ctypes
+from ctypes import c_char_p, c_double, c_float, c_int32, c_int64, c_uint64, c_void_p
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "liblongspark_amd.so"
+
+if not LIB_PATH.exists():
+    raise ImportError(
+        f"{LIB_PATH} is missing: build the HIP library first with "
+        "`python -m longspark_amd.build` (or __graft_entry__.build())")
+
+_lib = ctypes.CDLL(str(LIB_PATH))
+
+LS_OK, LS_ERR_SHAPE, LS_ERR_DTYPE, LS_ERR_ALIGN, LS_ERR_LAUNCH, LS_ERR_WORKSPACE, LS_ERR_VALUE = range(7)
+LS_F32, LS_BF16, LS_F16, LS_I32, LS_I64 = range(5)
+
+_DTYPES = {
+    torch.float32: LS_F32,
+    torch.bfloat16: LS_BF16,
+    torch.float16: LS_F16,
+    torch.int32: LS_I32,
+    torch.int64: LS_I64,
+}
+
+P, I32, I64, U64, F32, F64 = c_void_p, c_int32, c_int64, c_uint64, c_float, c_double
+
+# name -> (restype, argtypes).  Kept in the order of include/longspark_amd.h.
+_SIGNATURES = {
+    "ls_last_error": (c_char_p, []),
+    "ls_version": (c_char_p, []),
+    "ls_verify_greedy_workspace_bytes": (U64, [I64, I32, I64]),
+    "ls_verify_greedy": (I32, [P, I32, I64, P, I32, I64, I64, I32, I64, I32, I64, P, P, P, P, P, P, U64, P]),
+}
+
+for _name, (_res, _args) in _SIGNATURES.items():
+    _fn = getattr(_lib, _name)
+    _fn.restype = _res
+    _fn.argtypes = _args
+
+
+def lib():
+    return _lib
+
+
+def exported_symbols():
+    return list(_SIGNATURES)
+
+
+def check(status: int, what: str) -> None:
+    """Raise the reference's exception type for a non-zero C ABI status."""
+    if status == LS_OK:
+        return
+    msg = _lib.ls_last_error().decode(errors="replace")
+    if status == LS_ERR_LAUNCH:
+        raise RuntimeError(f"{what}: {msg}")
+    raise ValueError(f"{what}: {msg}")
+
+
+def call(name: str, *args) -> None:
+    check(getattr(_lib, name)(*args), name)
+
+
+def dtype_code(t: torch.Tensor) -> int:
+    try:
+        return _DTYPES[t.dtype]
+    except KeyError:
+        raise ValueError(f"unsupported dtype {t.dtype}") from None
+
+
+def ptr(t):
+    """Device address of a tensor (None for a missing optional tensor)."""
+    return None if t is None else t.data_ptr()
+
+
+def stream_of(device: torch.device):
+    """Raw hipStream_t of torch's current stream on ``device``."""
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def require_cuda(*tensors, what: str) -> torch.device:
+    """All given (non-None) tensors must live on one GPU; returns that device."""
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise ValueError(f"{what} requires GPU tensors (got a {t.device} tensor)")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"{what}: tensors on different devices ({dev} vs {t.device})")
+    if dev is None:
+        raise ValueError(f"{what}: no tensors given")
+    return dev
+
+
+class _Workspaces:
+    """Zero-initialised scratch buffers kept per (op, device, stream).
+
+    Every C ABI call leaves its workspace counters at zero, so a buffer is
+    allocated (zero-filled) once and reused; it only grows.
+    """
+
+    def __init__(self):
+        self._bufs = {}
+
+    def get(self, op: str, nbytes: int, device: torch.device) -> torch.Tensor:
+        key = (op, device.index, stream_of(device))
+        buf = self._bufs.get(key)
+        if buf is None or buf.numel() < nbytes:
+            buf = torch.zeros(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+            self._bufs[key] = buf
+        return buf
+
+
+workspaces = _Workspaces()

@@ -1,0 +1,102 @@
+"""Seeded synthetic inputs for the verify-and-refresh workloads.
+
+The workloads are the reference path's benchmark configurations:
+  greedy      -- greedy chain verification, logits ~ N(0, 3^2) bf16 with the
+                 drafted token boosted by +8 with probability 0.7;
+  stochastic  -- rejection-sampling verification with temperature / top-k /
+                 top-p (and optionally min-p, penalties over a Zipf history and
+                 a packed vocabulary bitmask); draft logits = target + N(0, 1)
+                 in fp32, drafted tokens sampled from the draft distribution q;
+  kv window   -- paged bf16 K/V pools with a random page permutation;
+  summary     -- learned summary queries, state, and new K/V rows.
+Every generator takes a seed and a device; the same seed gives the same
+inputs on every device (generation runs on the CPU generator unless
+``gen_device`` says otherwise).
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+
+VOCAB = 151936
+
+
+def _gen(seed: int, device) -> torch.Generator:
+    return torch.Generator(device=device).manual_seed(int(seed))
+
+
+def greedy_inputs(batch: int, width: int = 16, vocab: int = VOCAB, *, seed: int = 0,
+                  dtype=torch.bfloat16, device="cpu", gen_device="cpu", sigma: float = 3.0,
+                  boost: float = 8.0, p_boost: float = 0.7):
+    """Target logits ``[batch*width, vocab]`` and candidates ``[batch, width]`` int32.
+
+    ``candidates[:, 0]`` is the current token and ``candidates[:, 1:]`` the
+    drafted tokens, uniform over the vocabulary.  Row j of a request verifies
+    drafted token j+1; its logit gets ``+boost`` with probability ``p_boost``.
+    """
+    g = _gen(seed, gen_device)
+    logits = torch.randn(batch, width, vocab, generator=g, device=gen_device) * sigma
+    cand = torch.randint(0, vocab, (batch, width), generator=g, device=gen_device, dtype=torch.int64)
+    hit = (torch.rand(batch, width - 1, generator=g, device=gen_device) < p_boost).float() * boost
+    logits[:, :-1].scatter_add_(2, cand[:, 1:, None], hit[..., None])
+    logits = logits.to(dtype).reshape(batch * width, vocab)
+    return logits.to(device), cand.to(torch.int32).to(device)
+
+
+def zipf_history(batch: int, length: int, vocab: int = VOCAB, *, s: float = 1.1, seed: int = 0,
+                 device="cpu") -> torch.Tensor:
+    """``[batch, length]`` int32 token ids drawn Zipf(s) over ranks 1..vocab,
+    rank r mapped to a per-request random token id."""
+    g = _gen(seed, "cpu")
+    ranks = torch.arange(1, vocab + 1, dtype=torch.float64)
+    w = ranks.pow(-s)
+    w = w / w.sum()
+    draws = torch.multinomial(w.expand(batch, -1), length, replacement=True, generator=g)
+    perm = torch.stack([torch.randperm(vocab, generator=g) for _ in range(batch)])
+    return perm.gather(1, draws).to(torch.int32).to(device)
+
+
+def random_bitmask(rows: int, vocab: int = VOCAB, *, density: float = 0.3, seed: int = 0,
+                   force_tokens: Optional[torch.Tensor] = None, force_prob: float = 0.8,
+                   device="cpu") -> torch.Tensor:
+    """Packed int32 bitmask ``[rows, ceil(vocab/32)]`` with about ``density`` of bits set.
+
+    When ``force_tokens [rows]`` is given, that token's bit is set with
+    probability ``force_prob`` and cleared otherwise.
+    """
+    g = _gen(seed, "cpu")
+    words = (vocab + 31) // 32
+    bits = torch.rand(rows, words * 32, generator=g) < density
+    if force_tokens is not None:
+        keep = torch.rand(rows, generator=g) < force_prob
+        bits[torch.arange(rows), force_tokens.long().cpu()] = keep
+    weights = (torch.ones(32, dtype=torch.int64) << torch.arange(32))
+    packed = (bits.view(rows, words, 32).to(torch.int64) * weights).sum(-1)
+    packed = torch.where(packed >= 2**31, packed - 2**32, packed)
+    return packed.to(torch.int32).to(device)
+
+
+@dataclass
+class SamplingParams:
+    """Per-request sampling parameters as ``[B]`` tensors (top_k >= V, top_p >= 1
+    and min_p <= 0 disable the respective filter)."""
+    temperatures: torch.Tensor
+    top_ks: torch.Tensor
+    top_ps: torch.Tensor
+    min_ps: torch.Tensor
+
+    @staticmethod
+    def uniform(batch: int, *, temperature=1.0, top_k=VOCAB, top_p=1.0, min_p=0.0, device="cpu"):
+        return SamplingParams(
+            temperatures=torch.full((batch,), float(temperature), dtype=torch.float32, device=device),
+            top_ks=torch.full((batch,), int(top_k), dtype=torch.int32, device=device),
+            top_ps=torch.full((batch,), float(top_p), dtype=torch.float32, device=device),
+            min_ps=torch.full((batch,), float(min_p), dtype=torch.float32, device=device),
+        )
+
+    def to(self, device):
+        return SamplingParams(*(t.to(device) for t in (self.temperatures, self.top_ks, self.top_ps,
+                                                        self.min_ps)))

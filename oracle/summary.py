@@ -1,0 +1,92 @@
+"""CPU oracle for the Global16 summary refresh (test infrastructure only).
+
+Restates the reference's fp32 torch functions generically in the number of
+summary slots S, new rows W, query heads Hq and KV heads Hkv:
+  * position scores  -- SRT/speculative/global16_raw256_incremental.py:50-87
+  * accepted merge   -- SRT/speculative/global16_raw256_incremental.py:90-166
+  * full-prefix state (fp64 ground truth) -- the definition that
+    vendor/specforge/modeling/draft/global16_raw256.py:829-869
+    (``global_state_from_full_prefix``) computes and :871-915
+    (``commit_accepted_delta``) must reproduce incrementally.
+``SRT`` abbreviates ``vendor/sglang/python/sglang/srt``.  GQA maps query head
+h to KV head ``h // (Hq // Hkv)`` (consecutive groups share a KV head).
+"""
+
+from __future__ import annotations
+
+import torch
+
+
+def position_scores(global_query: torch.Tensor, new_keys: torch.Tensor, softmax_scale: float,
+                    softcap: float = 0.0) -> torch.Tensor:
+    """``[B, Hq, S, D]`` x ``[B, W, Hkv, D]`` -> ``[B, Hq, S, W]`` fp32 scores.
+
+    global16_raw256_incremental.py:76-87: fp32 einsum over D, times the scale,
+    then ``softcap * tanh(s / softcap)`` when softcap > 0 (:44-47).
+    """
+    batch, hq, rows, dim = global_query.shape
+    w, hkv = new_keys.shape[1], new_keys.shape[2]
+    groups = hq // hkv
+    q = global_query.float().reshape(batch, hkv, groups, rows, dim)
+    k = new_keys.float().permute(0, 2, 1, 3)
+    scores = torch.einsum("bhgrd,bhwd->bhgrw", q, k) * float(softmax_scale)
+    if softcap > 0:
+        scores = torch.tanh(scores / softcap) * softcap
+    return scores.reshape(batch, hq, rows, w)
+
+
+def merge_accepted_positions(state_output, state_lse, position_scores_, accepted_values, accept_lens):
+    """Online-softmax merge of the first ``accept_lens[b]`` rows into (output, lse).
+
+    global16_raw256_incremental.py:124-166 restated with W = ``accepted_values.shape[1]``:
+    masked scores, ``merged = logsumexp(stack(lse, logsumexp(scores)))``,
+    ``out = out * exp(lse - merged) + sum_w exp(s_w - merged) * v_w``.
+    """
+    batch, hq, rows, dim = state_output.shape
+    w = accepted_values.shape[1]
+    hkv = accepted_values.shape[2]
+    positions = torch.arange(w, dtype=accept_lens.dtype)
+    valid = positions[None, :] < accept_lens[:, None]
+    masked = position_scores_.float().masked_fill(~valid[:, None, None, :], float("-inf"))
+    merged_lse = torch.logsumexp(torch.stack((state_lse.float(), torch.logsumexp(masked, dim=-1))), dim=0)
+    prior_weight = torch.exp(state_lse.float() - merged_lse)
+    delta_weight = torch.exp(masked - merged_lse[..., None])
+    delta_weight = torch.where(valid[:, None, None, :], delta_weight, torch.zeros_like(delta_weight))
+    groups = hq // hkv
+    weights = delta_weight.view(batch, hkv, groups, rows, w)
+    values = accepted_values.float().permute(0, 2, 1, 3)
+    delta_out = torch.einsum("bhgrw,bhwd->bhgrd", weights, values).reshape(batch, hq, rows, dim)
+    return state_output.float() * prior_weight[..., None] + delta_out, merged_lse
+
+
+def full_prefix_state(global_query, keys, values, softmax_scale: float, dtype=torch.float64):
+    """Normalised attention output and LSE of every query row over a whole prefix.
+
+    ``keys``/``values`` are ``[B, T, Hkv, D]``.  This is the quantity the
+    incremental merge maintains: after folding every prefix row, the state must
+    equal ``softmax(scale * q k^T) v`` with ``lse = logsumexp(scale * q k^T)``.
+    """
+    batch, hq, rows, dim = global_query.shape
+    hkv = keys.shape[2]
+    groups = hq // hkv
+    q = global_query.to(dtype).reshape(batch, hkv, groups, rows, dim)
+    k = keys.to(dtype).permute(0, 2, 1, 3)
+    v = values.to(dtype).permute(0, 2, 1, 3)
+    s = torch.einsum("bhgrd,bhtd->bhgrt", q, k) * softmax_scale
+    lse = torch.logsumexp(s, dim=-1)
+    out = torch.einsum("bhgrt,bhtd->bhgrd", torch.softmax(s, dim=-1), v)
+    return out.reshape(batch, hq, rows, dim), lse.reshape(batch, hq, rows)
+
+
+def summary_update(state_output, state_lse, global_query, new_keys, new_values, accept_lens,
+                   softmax_scale: float, state_slots=None):
+    """Score + merge in one call, updating ``state_*[state_slots[b]]``; returns new copies."""
+    out = state_output.clone()
+    lse = state_lse.clone()
+    batch = new_keys.shape[0]
+    slots = torch.arange(batch) if state_slots is None else state_slots.long()
+    scores = position_scores(global_query, new_keys, softmax_scale)
+    o, l = merge_accepted_positions(out[slots], lse[slots], scores, new_values, accept_lens)
+    out[slots] = o
+    lse[slots] = l
+    return out, lse
