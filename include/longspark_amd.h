@@ -5,11 +5,15 @@
  * plus the hipStream_t to launch on (passed as void*), validates its
  * arguments on the host before launching anything, and returns an int status
  * (LS_OK = 0).  On failure, ls_last_error() returns a message for the calling
- * thread.  No entry point allocates device memory or synchronises the host:
- * scratch space is a caller-owned workspace whose size the matching
- * *_workspace_bytes() function reports.  A workspace must be zero-filled
- * before its first use; every call leaves its counters at zero again.  Calls
- * that share one workspace must not overlap (issue them on one stream).
+ * thread.  No entry point allocates device memory or synchronises the host.
+ * Scratch space is caller-owned and comes in two buffers whose sizes the
+ * matching *_workspace() function reports:
+ *   counters -- zero-filled before first use; every call returns every
+ *               counter it touched to zero, so one zeroed counter buffer can
+ *               be shared by all entry points issued on one stream;
+ *   scratch  -- no initialisation required.
+ * Calls that share a counter or scratch buffer must not overlap (issue them
+ * on one stream).
  *
  * Reference paths below are relative to the LongSpark repository root;
  * SRT = vendor/sglang/python/sglang/srt.
@@ -85,13 +89,14 @@ LS_API const char* ls_version(void);
  * Ties resolve to the lowest index (torch.argmax).  NaN logits are not
  * supported.
  * ------------------------------------------------------------------------- */
-LS_API uint64_t ls_verify_greedy_workspace_bytes(int64_t batch, int32_t width, int64_t vocab);
+LS_API int ls_verify_greedy_workspace(int64_t batch, int32_t width, int64_t vocab,
+                                      uint64_t* counter_bytes, uint64_t* scratch_bytes);
 LS_API int ls_verify_greedy(const void* logits, int32_t logits_dtype, int64_t logits_row_stride,
                      const void* candidates, int32_t candidates_dtype, int64_t cand_stride_b,
                      int64_t cand_stride_k, int32_t cand_first_col, int64_t batch, int32_t width,
                      int64_t vocab, const int32_t* cutoff_verify_lens, int32_t* accept_lens,
-                     int64_t* bonus, int32_t* truth, int32_t* cap_trim, void* workspace,
-                     uint64_t workspace_bytes, void* stream);
+                     int64_t* bonus, int32_t* truth, int32_t* cap_trim, void* counters,
+                     uint64_t counter_bytes, void* scratch, uint64_t scratch_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -41,8 +41,9 @@ P, I32, I64, U64, F32, F64 = c_void_p, c_int32, c_int64, c_uint64, c_float, c_do
 _SIGNATURES = {
     "ls_last_error": (c_char_p, []),
     "ls_version": (c_char_p, []),
-    "ls_verify_greedy_workspace_bytes": (U64, [I64, I32, I64]),
-    "ls_verify_greedy": (I32, [P, I32, I64, P, I32, I64, I64, I32, I64, I32, I64, P, P, P, P, P, P, U64, P]),
+    "ls_verify_greedy_workspace": (I32, [I64, I32, I64, P, P]),
+    "ls_verify_greedy": (I32, [P, I32, I64, P, I32, I64, I64, I32, I64, I32, I64, P, P, P, P, P,
+                               P, U64, P, U64, P]),
 }
 
 for _name, (_res, _args) in _SIGNATURES.items():
@@ -107,23 +108,37 @@ def require_cuda(*tensors, what: str) -> torch.device:
     return dev
 
 
-class _Workspaces:
-    """Zero-initialised scratch buffers kept per (op, device, stream).
+def workspace_sizes(fn_name: str, *args):
+    """Call a ``*_workspace`` query; returns (counter_bytes, scratch_bytes)."""
+    c, s = ctypes.c_uint64(0), ctypes.c_uint64(0)
+    call(fn_name, *args, ctypes.byref(c), ctypes.byref(s))
+    return c.value, s.value
 
-    Every C ABI call leaves its workspace counters at zero, so a buffer is
-    allocated (zero-filled) once and reused; it only grows.
+
+class _Workspaces:
+    """Scratch and counter buffers kept per (device, stream).
+
+    The counter buffer is zero-filled when (re)allocated and every C ABI call
+    leaves it zero, so one buffer serves every entry point on a stream.
+    Buffers only grow; growing reallocates (zero-filled for counters).
     """
 
     def __init__(self):
         self._bufs = {}
 
-    def get(self, op: str, nbytes: int, device: torch.device) -> torch.Tensor:
-        key = (op, device.index, stream_of(device))
+    def _get(self, kind: str, nbytes: int, device: torch.device) -> torch.Tensor:
+        key = (kind, device.index, stream_of(device))
         buf = self._bufs.get(key)
         if buf is None or buf.numel() < nbytes:
-            buf = torch.zeros(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+            n = max(int(nbytes), 4096)
+            buf = torch.zeros(n, dtype=torch.uint8, device=device) if kind == "counters" else \
+                torch.empty(n, dtype=torch.uint8, device=device)
             self._bufs[key] = buf
         return buf
+
+    def get(self, counter_bytes: int, scratch_bytes: int, device: torch.device):
+        """(counters, scratch) uint8 tensors of at least the given sizes."""
+        return self._get("counters", counter_bytes, device), self._get("scratch", scratch_bytes, device)
 
 
 workspaces = _Workspaces()

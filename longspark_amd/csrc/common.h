@@ -150,16 +150,59 @@ __device__ __forceinline__ MaxSum maxsum_merge(MaxSum a, MaxSum b) {
 }
 
 // -------------------------------------------------- cross-workgroup sync ---
+//
+// gfx950 has one L2 per XCD and the L2s are not coherent with each other, so
+// a device-scope fence (__threadfence) writes back and invalidates the whole
+// L2 of the issuing XCD -- far too expensive to do once per workgroup.  The
+// kernels here therefore pass every cross-workgroup value through agent-scope
+// atomic read-modify-write operations, which are performed at the single
+// coherence point of their address:
+//   * producers publish with an atomic RMW (max / add / exchange) and wait for
+//     it to complete (its return value) before arriving on a counter;
+//   * the last arriver reads the published words with atomic RMWs too
+//     (exchange with 0, which also returns them to zero for the next launch).
+// Completion of the producer's RMW precedes its counter increment, which
+// precedes the last arriver's increment and therefore its reads, so the reads
+// observe every published value.  No L2 maintenance is needed.
 
-// Agent-scope counter increment with acquire-release ordering.  Returns the
-// previous value.  Writes made by the calling thread before the call are
-// visible to whichever thread observes the incremented value.
-__device__ __forceinline__ uint32_t arrive(uint32_t* counter) {
-  __threadfence();
-  return __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ void wait_vm() { __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup"); }
+
+__device__ __forceinline__ uint32_t atomic_add_u32(uint32_t* p, uint32_t v) {
+  return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ void reset_counter(uint32_t* counter) {
-  __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ uint64_t atomic_max_u64(uint64_t* p, uint64_t v) {
+  return __hip_atomic_fetch_max(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t atomic_take_u64(uint64_t* p) {
+  return __hip_atomic_exchange(p, uint64_t(0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t atomic_take_u32(uint32_t* p) {
+  return __hip_atomic_exchange(p, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Arrive on a counter after this thread's prior atomics completed; returns
+// the previous count.
+__device__ __forceinline__ uint32_t arrive(uint32_t* counter) {
+  wait_vm();
+  return atomic_add_u32(counter, 1u);
+}
+
+// Order-preserving map of fp32 to uint32 (larger float -> larger integer;
+// -0 is canonicalised to +0 so that the two compare equal, as floats do).
+__device__ __forceinline__ uint32_t ordered_f32(float x) {
+  uint32_t b = __float_as_uint(x + 0.0f);
+  return b ^ (static_cast<uint32_t>(static_cast<int32_t>(b) >> 31) | 0x80000000u);
+}
+__device__ __forceinline__ float unordered_f32(uint32_t k) {
+  uint32_t b = (k & 0x80000000u) ? (k ^ 0x80000000u) : ~k;
+  return __uint_as_float(b);
+}
+// Packed argmax key: larger value wins, then the lower index.  Every real key
+// is non-zero, so 0 is the neutral "nothing published" value.
+__device__ __forceinline__ uint64_t argmax_key(float v, int idx) {
+  return (static_cast<uint64_t>(ordered_f32(v)) << 32) | (0xffffffffu - static_cast<uint32_t>(idx));
+}
+__device__ __forceinline__ int argmax_key_index(uint64_t key) {
+  return static_cast<int>(0xffffffffu - static_cast<uint32_t>(key));
 }
 
 // Index of the current 16-byte vector range owned by one slice of a row.

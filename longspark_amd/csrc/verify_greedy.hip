@@ -2,9 +2,11 @@
 // accepted prefix and the bonus token of each request.
 //
 // Grid: rows * slices workgroups of 256 threads.  A workgroup streams one
-// slice of one row with 16-byte loads and reduces it to (max, first index).
-// The last workgroup to finish a row merges the row's slices; the last row to
-// finish a request compares its drafted tokens with the row argmaxes.
+// slice of one row with 16-byte loads and reduces it to (max, first index),
+// which it folds into the row's packed argmax key with one atomic max.  The
+// last workgroup to finish a request (counted on a per-request counter) takes
+// the request's row keys -- returning them to zero -- and compares the drafted
+// tokens with the row argmaxes.
 //
 // Reference semantics: src/longspark/engine/target.py:474-477 and
 // vendor/sglang/python/sglang/srt/speculative/dflash_utils.py:564-602.
@@ -29,29 +31,22 @@ int greedy_slices(int64_t rows, int64_t vocab) {
 }
 
 struct GreedyWs {
-  ArgMax* partials;    // [rows * slices]
-  int32_t* truth;      // [rows]
-  uint32_t* row_cnt;   // [rows]
-  uint32_t* req_cnt;   // [batch]
+  uint64_t* row_key;   // counters: [rows] packed argmax keys, zero at rest
+  uint32_t* req_cnt;   // counters: [batch] finished workgroups per request
 };
 
-uint64_t greedy_ws_bytes(int64_t batch, int64_t rows, int slices) {
-  auto up = [](uint64_t x) { return (x + 255) & ~uint64_t(255); };
-  return up(sizeof(ArgMax) * rows * slices) + up(4 * rows) + up(4 * rows) + up(4 * batch);
+inline uint64_t up256(uint64_t x) { return (x + 255) & ~uint64_t(255); }
+
+void greedy_ws_sizes(int64_t batch, int64_t rows, uint64_t* counters, uint64_t* scratch) {
+  *counters = up256(8 * rows) + up256(4 * batch);
+  *scratch = 0;
 }
 
-GreedyWs greedy_ws(void* base, int64_t batch, int64_t rows, int slices) {
-  auto up = [](uint64_t x) { return (x + 255) & ~uint64_t(255); };
-  char* p = static_cast<char*>(base);
+GreedyWs greedy_ws(void* counters, int64_t rows) {
   GreedyWs w;
-  w.partials = reinterpret_cast<ArgMax*>(p);
-  p += up(sizeof(ArgMax) * rows * slices);
-  w.truth = reinterpret_cast<int32_t*>(p);
-  p += up(4 * rows);
-  w.row_cnt = reinterpret_cast<uint32_t*>(p);
-  p += up(4 * rows);
-  w.req_cnt = reinterpret_cast<uint32_t*>(p);
-  (void)batch;
+  char* c = static_cast<char*>(counters);
+  w.row_key = reinterpret_cast<uint64_t*>(c);
+  w.req_cnt = reinterpret_cast<uint32_t*>(c + up256(8 * rows));
   return w;
 }
 
@@ -118,7 +113,7 @@ __global__ __launch_bounds__(kThreads) void greedy_verify_kernel(
     int32_t* __restrict__ accept_out, int64_t* __restrict__ bonus_out, int32_t* __restrict__ truth_out,
     int32_t* __restrict__ trim_out) {
   __shared__ ArgMax red[kThreads / kWave];
-  __shared__ int is_last;
+  __shared__ int t[64];  // row argmaxes of the request (last workgroup only)
   const int64_t row = blockIdx.x / slices;
   const int slice = blockIdx.x % slices;
   const SliceRange r = slice_range(vocab, slices, slice, Tag::kPerVec);
@@ -130,59 +125,52 @@ __global__ __launch_bounds__(kThreads) void greedy_verify_kernel(
   const int wid = threadIdx.x / kWave;
   if (lane == 0) red[wid] = best;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    ArgMax m = red[0];
-#pragma unroll
-    for (int w = 1; w < kThreads / kWave; ++w) m = argmax_merge(m, red[w]);
-    ws.partials[row * slices + slice] = m;
-    is_last = (arrive(&ws.row_cnt[row]) == static_cast<uint32_t>(slices - 1));
-  }
-  __syncthreads();
-  if (!is_last) return;
+  if (threadIdx.x != 0) return;
 
-  // Last slice of this row: merge the row's partials in wave 0.
-  if (threadIdx.x < kWave) {
-    __threadfence();
-    ArgMax m{-INFINITY, 0x7fffffff};
-    for (int s = threadIdx.x; s < slices; s += kWave) m = argmax_merge(m, ws.partials[row * slices + s]);
-    m = wave_argmax(m);
-    if (threadIdx.x == 0) {
-      reset_counter(&ws.row_cnt[row]);
-      ws.truth[row] = m.i;
-      if (truth_out) truth_out[row] = m.i;
-      const int64_t req = row / width;
-      if (arrive(&ws.req_cnt[req]) == static_cast<uint32_t>(width - 1)) {
-        // Last row of this request: accepted prefix and bonus.
-        __threadfence();
-        reset_counter(&ws.req_cnt[req]);
-        const int32_t* t = ws.truth + req * width;
-        int len = 0;
-        while (len < width - 1 &&
-               static_cast<int64_t>(cand[req * csb + static_cast<int64_t>(first_col + len) * csk]) ==
-                   static_cast<int64_t>(__hip_atomic_load(t + len, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)))
-          ++len;
-        int trim = 0;
-        if (cutoff) {
-          int cap = cutoff[req] - 1;
-          cap = cap < 0 ? 0 : (cap > width - 1 ? width - 1 : cap);
-          if (len > cap) { trim = len - cap; len = cap; }
-        }
-        if (trim_out) trim_out[req] = trim;
-        accept_out[req] = len;
-        bonus_out[req] = __hip_atomic_load(t + len, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
+  ArgMax m = red[0];
+#pragma unroll
+  for (int w = 1; w < kThreads / kWave; ++w) m = argmax_merge(m, red[w]);
+  if (m.i != 0x7fffffff) atomic_max_u64(&ws.row_key[row], argmax_key(m.v, m.i));
+  const int64_t req = row / width;
+  const uint32_t per_req = static_cast<uint32_t>(width) * static_cast<uint32_t>(slices);
+  if (arrive(&ws.req_cnt[req]) != per_req - 1) return;
+
+  // Last workgroup of this request: take the row keys (resetting them), then
+  // the accepted prefix and the bonus token.
+  atomic_take_u32(&ws.req_cnt[req]);
+  int len = 0;
+  bool matching = true;
+  for (int j = 0; j < width; ++j) {
+    const int idx = argmax_key_index(atomic_take_u64(&ws.row_key[req * width + j]));
+    t[j] = idx;
+    if (truth_out) truth_out[req * width + j] = idx;
+    if (matching && j < width - 1) {
+      if (static_cast<int64_t>(cand[req * csb + static_cast<int64_t>(first_col + j) * csk]) == idx)
+        ++len;
+      else
+        matching = false;
     }
   }
+  int trim = 0;
+  if (cutoff) {
+    int cap = cutoff[req] - 1;
+    cap = cap < 0 ? 0 : (cap > width - 1 ? width - 1 : cap);
+    if (len > cap) { trim = len - cap; len = cap; }
+  }
+  if (trim_out) trim_out[req] = trim;
+  accept_out[req] = len;
+  bonus_out[req] = t[len];
 }
 
 template <typename Tag, typename CandT>
 int launch_greedy(const void* logits, int64_t row_stride, const void* cand, int64_t csb, int64_t csk,
                   int first_col, int64_t batch, int width, int64_t vocab, const int32_t* cutoff,
-                  int32_t* accept, int64_t* bonus, int32_t* truth, int32_t* trim, void* workspace,
-                  hipStream_t stream) {
+                  int32_t* accept, int64_t* bonus, int32_t* truth, int32_t* trim, void* counters,
+                  void* scratch, hipStream_t stream) {
   const int64_t rows = batch * width;
   const int slices = greedy_slices(rows, vocab);
-  GreedyWs ws = greedy_ws(workspace, batch, rows, slices);
+  GreedyWs ws = greedy_ws(counters, rows);
+  (void)scratch;
   using S = typename Tag::storage;
   const bool vec = aligned16(logits) && ((row_stride * sizeof(S)) % 16 == 0);
   dim3 grid(static_cast<unsigned>(rows * slices));
@@ -201,21 +189,25 @@ int launch_greedy(const void* logits, int64_t row_stride, const void* cand, int6
 }  // namespace
 }  // namespace ls
 
-extern "C" uint64_t ls_verify_greedy_workspace_bytes(int64_t batch, int32_t width, int64_t vocab) {
-  if (batch <= 0 || width <= 0 || vocab <= 0) return 0;
+extern "C" int ls_verify_greedy_workspace(int64_t batch, int32_t width, int64_t vocab,
+                                         uint64_t* counter_bytes, uint64_t* scratch_bytes) {
+  LS_CHECK(batch > 0 && width > 0 && vocab > 0 && counter_bytes && scratch_bytes, LS_ERR_SHAPE,
+           "ls_verify_greedy_workspace: need positive sizes and output pointers");
   const int64_t rows = batch * width;
-  return ls::greedy_ws_bytes(batch, rows, ls::greedy_slices(rows, vocab));
+  ls::greedy_ws_sizes(batch, rows, counter_bytes, scratch_bytes);
+  return LS_OK;
 }
 
 extern "C" int ls_verify_greedy(const void* logits, int32_t logits_dtype, int64_t logits_row_stride,
                                 const void* candidates, int32_t candidates_dtype, int64_t cand_stride_b,
                                 int64_t cand_stride_k, int32_t cand_first_col, int64_t batch, int32_t width,
                                 int64_t vocab, const int32_t* cutoff_verify_lens, int32_t* accept_lens,
-                                int64_t* bonus, int32_t* truth, int32_t* cap_trim, void* workspace,
-                                uint64_t workspace_bytes, void* stream) {
+                                int64_t* bonus, int32_t* truth, int32_t* cap_trim, void* counters,
+                                uint64_t counter_bytes, void* scratch, uint64_t scratch_bytes,
+                                void* stream) {
   using namespace ls;
-  LS_CHECK(batch > 0 && width >= 2 && vocab > 0, LS_ERR_SHAPE,
-           "ls_verify_greedy: need batch > 0, width >= 2, vocab > 0 (got %lld, %d, %lld)",
+  LS_CHECK(batch > 0 && width >= 2 && width <= 64 && vocab > 0, LS_ERR_SHAPE,
+           "ls_verify_greedy: need batch > 0, 2 <= width <= 64, vocab > 0 (got %lld, %d, %lld)",
            (long long)batch, width, (long long)vocab);
   LS_CHECK(vocab < (int64_t(1) << 31), LS_ERR_SHAPE, "ls_verify_greedy: vocab must fit int32");
   LS_CHECK(logits_row_stride >= vocab, LS_ERR_SHAPE, "ls_verify_greedy: row stride %lld < vocab %lld",
@@ -223,21 +215,24 @@ extern "C" int ls_verify_greedy(const void* logits, int32_t logits_dtype, int64_
   LS_CHECK(cand_first_col == 0 || cand_first_col == 1, LS_ERR_VALUE,
            "ls_verify_greedy: cand_first_col must be 0 or 1");
   LS_CHECK(logits && candidates && accept_lens && bonus, LS_ERR_VALUE, "ls_verify_greedy: null pointer");
-  const uint64_t need = ls_verify_greedy_workspace_bytes(batch, width, vocab);
-  LS_CHECK(workspace && workspace_bytes >= need, LS_ERR_WORKSPACE,
-           "ls_verify_greedy: workspace of %llu bytes required", (unsigned long long)need);
+  uint64_t need_c = 0, need_s = 0;
+  ls_verify_greedy_workspace(batch, width, vocab, &need_c, &need_s);
+  LS_CHECK(counters && counter_bytes >= need_c && (need_s == 0 || (scratch && scratch_bytes >= need_s)),
+           LS_ERR_WORKSPACE,
+           "ls_verify_greedy: needs %llu counter bytes and %llu scratch bytes",
+           (unsigned long long)need_c, (unsigned long long)need_s);
   hipStream_t s = static_cast<hipStream_t>(stream);
 #define LS_GREEDY_CAND(TAG)                                                                          \
   if (candidates_dtype == LS_I32)                                                                    \
     return launch_greedy<TAG, int32_t>(logits, logits_row_stride, candidates, cand_stride_b,         \
                                        cand_stride_k, cand_first_col, batch, width, vocab,           \
                                        cutoff_verify_lens, accept_lens, bonus, truth, cap_trim,     \
-                                       workspace, s);                     \
+                                       counters, scratch, s);                     \
   if (candidates_dtype == LS_I64)                                                                    \
     return launch_greedy<TAG, int64_t>(logits, logits_row_stride, candidates, cand_stride_b,         \
                                        cand_stride_k, cand_first_col, batch, width, vocab,           \
                                        cutoff_verify_lens, accept_lens, bonus, truth, cap_trim,     \
-                                       workspace, s);                     \
+                                       counters, scratch, s);                     \
   return fail(LS_ERR_DTYPE, "ls_verify_greedy: candidates must be int32 or int64");
   if (logits_dtype == LS_BF16) { LS_GREEDY_CAND(BF16) }
   if (logits_dtype == LS_F16) { LS_GREEDY_CAND(F16) }

@@ -61,13 +61,13 @@ def verify_greedy(*, logits: torch.Tensor, candidates: torch.Tensor, width: int,
     bonus = torch.empty(batch, dtype=torch.int64, device=dev)
     trim = torch.empty(batch, dtype=torch.int32, device=dev)
     truth = torch.empty(batch * width, dtype=torch.int32, device=dev) if return_truth else None
-    nbytes = _lib.lib().ls_verify_greedy_workspace_bytes(batch, width, vocab)
-    ws = _lib.workspaces.get("greedy", nbytes, dev)
+    cnt, scr = _lib.workspaces.get(*_lib.workspace_sizes("ls_verify_greedy_workspace", batch, width, vocab),
+                                   dev)
     _lib.call("ls_verify_greedy", logits.data_ptr(), _lib.dtype_code(logits), logits.stride(0),
               candidates.data_ptr(), _lib.dtype_code(candidates), candidates.stride(0),
               candidates.stride(1), cand_first_col, batch, width, vocab,
               _lib.ptr(cutoff_verify_lens), accept.data_ptr(), bonus.data_ptr(), _lib.ptr(truth),
-              trim.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_of(dev))
+              trim.data_ptr(), cnt.data_ptr(), cnt.numel(), scr.data_ptr(), scr.numel(), _lib.stream_of(dev))
     if return_truth:
         return accept, bonus, trim, truth
     return accept, bonus, trim

@@ -45,21 +45,22 @@ def test_greedy_host_validation_codes():
     dummy = ctypes.c_void_p(16)
     # width < 2
     st = lib.ls_verify_greedy(dummy, _lib.LS_BF16, 100, dummy, _lib.LS_I32, 16, 1, 1, 4, 1, 100,
-                              None, dummy, dummy, None, None, dummy, 1 << 20, None)
+                              None, dummy, dummy, None, None, dummy, 1 << 20, dummy, 1 << 20, None)
     assert st == _lib.LS_ERR_SHAPE and b"width" in lib.ls_last_error()
     # row stride smaller than vocab
     st = lib.ls_verify_greedy(dummy, _lib.LS_BF16, 10, dummy, _lib.LS_I32, 16, 1, 1, 4, 16, 100,
-                              None, dummy, dummy, None, None, dummy, 1 << 20, None)
+                              None, dummy, dummy, None, None, dummy, 1 << 20, dummy, 1 << 20, None)
     assert st == _lib.LS_ERR_SHAPE
     # bad dtype
     st = lib.ls_verify_greedy(dummy, 99, 100, dummy, _lib.LS_I32, 16, 1, 1, 4, 16, 100,
-                              None, dummy, dummy, None, None, dummy, 1 << 20, None)
+                              None, dummy, dummy, None, None, dummy, 1 << 20, dummy, 1 << 20, None)
     assert st == _lib.LS_ERR_DTYPE
     # workspace too small
     st = lib.ls_verify_greedy(dummy, _lib.LS_BF16, 100, dummy, _lib.LS_I32, 16, 1, 1, 4, 16, 100,
-                              None, dummy, dummy, None, None, dummy, 4, None)
+                              None, dummy, dummy, None, None, dummy, 4, dummy, 4, None)
     assert st == _lib.LS_ERR_WORKSPACE
-    assert lib.ls_verify_greedy_workspace_bytes(128, 16, 151936) > 0
+    c, s = _lib.workspace_sizes("ls_verify_greedy_workspace", 128, 16, 151936)
+    assert c > 0 and s == 0
 
 
 def test_python_wrappers_reject_cpu_tensors():
