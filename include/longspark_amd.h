@@ -98,6 +98,146 @@ LS_API int ls_verify_greedy(const void* logits, int32_t logits_dtype, int64_t lo
                      int64_t* bonus, int32_t* truth, int32_t* cap_trim, void* counters,
                      uint64_t counter_bytes, void* scratch, uint64_t scratch_bytes, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * Penalty tables from each request's output-token history.
+ *
+ * Compact form of the accumulated [B, V] penalty tensors the reference keeps
+ * (SRT/sampling/penaltylib/frequency_penalty.py:35-43,
+ * presence_penalty.py:35-43, repetition_penalty.py:48-57,
+ * orchestrator.py:87-104; consumed at SRT/sampling/sampling_batch_info.py:
+ * 269-286):
+ *   bits[b, w]  presence bitmap of history b (token v -> bit v&31 of word v>>5),
+ *   rank[b, w]  number of present tokens below token 32*w,
+ *   add[b, r]   additive penalty of the r-th present token in ascending token
+ *               order: (0 - F) - P, F = fp32 sum of frequency[b] repeated
+ *               count times, P = presence[b] (null frequency/presence = 0).
+ * history: [batch, >= history_cap] int32 with row stride history_stride;
+ *   history_lens (int32 [batch], may be NULL = history_cap) entries per row.
+ *   Ids outside [0, vocab) are ignored.
+ * words_stride >= ceil(vocab/32); add_stride >= history_cap.
+ * distinct (int32 [batch], may be NULL) receives the number of present tokens.
+ * Limit: 8*ceil(vocab/32) + 4*history_cap <= 64 KiB.
+ * ------------------------------------------------------------------------- */
+LS_API int ls_penalty_tables(const int32_t* history, int64_t history_stride, const int32_t* history_lens,
+                             int64_t batch, int32_t history_cap, int64_t vocab, const float* frequency,
+                             const float* presence, uint32_t* bits, uint32_t* rank, int64_t words_stride,
+                             float* add, int64_t add_stride, int32_t* distinct, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * In-place logit adjustment of [rows, vocab] logits: penalties (tables from
+ * ls_penalty_tables, repetition[b] scaling of present tokens) and the packed
+ * vocabulary bitmask (bit 0 -> -inf, LSB first; only the first
+ * min(vocab, 32*mask_words) columns are masked).
+ *
+ * Replaces SRT/speculative/dflash_utils.py:127-213
+ * (apply_dflash_verify_logits_adjustments: verify_quirk = 1 builds the bias
+ * on a zero tensor as that function does, verify_quirk = 0 applies the
+ * penalties to the logits themselves in the order of
+ * SRT/sampling/sampling_batch_info.py:269-286) and, with no penalty tables,
+ * SRT/constrained/triton_ops/bitmask_ops.py:84-141
+ * (apply_token_bitmask_inplace_triton).
+ * rows_per_request: rows of one request (penalty table b = row / rows_per_request);
+ * mask_rows_per_request: 1 (one mask row per logits row) or rows_per_request
+ * (one mask row per request).  Arithmetic is fp32; bf16/fp16 rows are rounded
+ * once per changed element.
+ * ------------------------------------------------------------------------- */
+LS_API int ls_adjust_logits(void* logits, int32_t logits_dtype, int64_t row_stride, int64_t rows, int64_t vocab,
+                            int32_t rows_per_request, const uint32_t* pen_bits, const uint32_t* pen_rank,
+                            int64_t pen_words_stride, const float* pen_add, int64_t pen_add_stride,
+                            const float* repetition, int32_t verify_quirk, const int32_t* vocab_mask,
+                            int64_t mask_stride, int32_t mask_rows_per_request, int64_t mask_words, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Fused stochastic chain verification of a drafted block.
+ *
+ * Replaces, in one call, the sequence
+ *   SRT/speculative/dflash_utils.py:127-213   logit adjustments (penalties, mask),
+ *   SRT/speculative/dflash_utils.py:743-810   target distribution (T, top-k, top-p)
+ *                                               + min-p (SRT/layers/sampler.py:238-242),
+ *   SRT/speculative/dspark_components/kernels/accept_sampling.py:259-567
+ *                                               single-q acceptance, residual, bonus
+ *                                               (q_mode 0), or
+ *   SRT/speculative/reject_sampling.py:5-204   dense-q chain sampling (q_mode 1),
+ *   src/longspark/engine/sampling.py:19-57     decide_acceptance + finish_sampling,
+ * with host-supplied uniforms.
+ *
+ * Target: logits [batch*width, vocab] (bf16/fp16/fp32), row r = request
+ *   r / width, position r % width; row j < width-1 verifies drafted token j at
+ *   candidates[b*cand_stride_b + (cand_first_col + j)*cand_stride_k].
+ * Sampling parameters per request ([batch]): temperatures (> 0, required),
+ *   top_ks (int32, >= vocab disables; NULL = disabled), top_ps (>= 1 disables),
+ *   min_ps (<= 0 disables).  max_top_k: host upper bound of top_ks (0 = 1024);
+ *   top-k above 1024 is not supported.
+ * Penalties (optional): tables from ls_penalty_tables, pen_repetition [batch]
+ *   (NULL = 1); pen_verify_quirk as in ls_adjust_logits.
+ * vocab_mask (optional): int32 words, mask_row_stride >= ceil(vocab/32);
+ *   mask_per_request = 1: row b, else row r.
+ * Draft: q_mode 0 -- draft_token_probs [batch, width-1] fp32 (q of each drafted
+ *   token) and draft rows [batch, width-1, vocab] (fp32 or bf16 logits; the q
+ *   row at the rejection is softmax(row / T_d) after the draft_* top-k / top-p
+ *   / min-p, each NULL = disabled, draft_temperatures NULL = temperatures);
+ *   q_mode 1 -- draft rows are fp32 probabilities [batch, width-1, vocab].
+ * Uniforms: uniforms [batch, width-1] (row stride uniform_stride_b),
+ *   final_uniforms [batch].
+ * Outputs: accept_lens[b] (int32) accepted drafted tokens, bonus[b] (int64)
+ *   the token drawn from the residual (rejection) or from the last row (all
+ *   accepted); p_cand_out [batch, width-1] (may be NULL) the target
+ *   probability of each drafted token.  A request whose support exceeds the
+ *   kernel's candidate capacity gets accept = bonus = -1 and ORs 1 into
+ *   *status (may be NULL).
+ * ------------------------------------------------------------------------- */
+typedef struct {
+  const void* logits;
+  int32_t logits_dtype;
+  int64_t logits_row_stride;
+  const void* candidates;
+  int32_t candidates_dtype;
+  int64_t cand_stride_b;
+  int64_t cand_stride_k;
+  int32_t cand_first_col;
+  int64_t batch;
+  int32_t width;
+  int64_t vocab;
+  const float* temperatures;
+  const int32_t* top_ks;
+  const float* top_ps;
+  const float* min_ps;
+  int32_t max_top_k;
+  const uint32_t* pen_bits;
+  const uint32_t* pen_rank;
+  int64_t pen_words_stride;
+  const float* pen_add;
+  int64_t pen_add_stride;
+  const float* pen_repetition;
+  int32_t pen_verify_quirk;
+  const int32_t* vocab_mask;
+  int64_t mask_row_stride;
+  int32_t mask_per_request;
+  int32_t q_mode;
+  const float* draft_token_probs;
+  int64_t dtp_stride_b;
+  const void* draft;
+  int32_t draft_dtype;
+  int64_t draft_stride_b;
+  int64_t draft_stride_k;
+  const float* draft_temperatures;
+  const int32_t* draft_top_ks;
+  const float* draft_top_ps;
+  const float* draft_min_ps;
+  const float* uniforms;
+  int64_t uniform_stride_b;
+  const float* final_uniforms;
+  int32_t* accept_lens;
+  int64_t* bonus;
+  float* p_cand_out;
+  int32_t* status;
+} ls_verify_sample_args;
+
+LS_API int ls_verify_sample_workspace(int64_t batch, int32_t width, int64_t vocab, int32_t max_top_k,
+                                      uint64_t* counter_bytes, uint64_t* scratch_bytes);
+LS_API int ls_verify_sample(const ls_verify_sample_args* args, void* counters, uint64_t counter_bytes,
+                            void* scratch, uint64_t scratch_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -11,6 +11,7 @@
 
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
+#include <float.h>
 #include <stdint.h>
 
 #include "../../include/longspark_amd.h"
@@ -53,6 +54,21 @@ __device__ __forceinline__ float to_f32<uint16_t>(uint16_t v) {  // bf16 bit pat
 }
 template <>
 __device__ __forceinline__ float to_f32<__half>(__half v) { return __half2float(v); }
+
+// fp32 -> storage type with round-to-nearest-even.
+template <typename T>
+__device__ __forceinline__ T from_f32(float v);
+template <>
+__device__ __forceinline__ float from_f32<float>(float v) { return v; }
+template <>
+__device__ __forceinline__ uint16_t from_f32<uint16_t>(float v) {
+  uint32_t b = __float_as_uint(v);
+  if ((b & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((b >> 16) | 0x40u);  // quiet NaN
+  b += 0x7fffu + ((b >> 16) & 1u);
+  return static_cast<uint16_t>(b >> 16);
+}
+template <>
+__device__ __forceinline__ __half from_f32<__half>(float v) { return __float2half(v); }
 
 // Storage tags: the element type a kernel template is instantiated for.
 struct BF16 { using storage = uint16_t; static constexpr int kPerVec = 8; };

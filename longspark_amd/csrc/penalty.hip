@@ -1,0 +1,179 @@
+// Penalty tables from an output-token history, and the standalone in-place
+// logit adjustment (penalties + vocabulary bitmask).
+//
+// The tables describe, per request, the accumulated penalties the reference
+// penalisers hold as dense [B, V] tensors
+// (vendor/sglang/python/sglang/srt/sampling/penaltylib/{frequency,presence,
+// repetition}_penalty.py, orchestrator.py:87-104), in a compact form:
+//   bits[b, w]  presence bitmap of the history (bit v & 31 of word v >> 5);
+//   rank[b, w]  number of present tokens below token 32*w;
+//   add[b, r]   additive penalty of the r-th present token (ascending token
+//               order): (0 - F) - P with F the fp32 sum of `frequency`
+//               repeated count times (scatter_add_ of identical values) and P
+//               the presence value, exactly as the reference accumulates it.
+// A token v is present iff its bit is set; its table entry is
+// add[b, rank[b, v>>5] + popcount(bits[b, v>>5] & ((1 << (v&31)) - 1))].
+#include "rowscan.h"
+
+namespace ls {
+namespace {
+
+constexpr int kPT = 256;
+
+__global__ __launch_bounds__(kPT) void penalty_tables_kernel(
+    const int32_t* __restrict__ hist, int64_t hist_stride, const int32_t* __restrict__ hist_lens, int hist_cap,
+    int64_t vocab, int words, const float* __restrict__ freq, const float* __restrict__ pres,
+    uint32_t* __restrict__ bits_out, uint32_t* __restrict__ rank_out, int64_t words_stride,
+    float* __restrict__ add_out, int64_t add_stride, int32_t* __restrict__ distinct_out) {
+  extern __shared__ uint32_t lds[];
+  uint32_t* bits = lds;              // [words]
+  uint32_t* rank = lds + words;      // [words]
+  uint32_t* cnt = lds + 2 * words;   // [hist_cap]
+  __shared__ uint32_t wave_tot[kPT / kWave];
+  const int b = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int n = hist_lens ? min(max(hist_lens[b], 0), hist_cap) : hist_cap;
+  const int32_t* h = hist + static_cast<int64_t>(b) * hist_stride;
+
+  for (int w = tid; w < words; w += kPT) bits[w] = 0;
+  for (int r = tid; r < hist_cap; r += kPT) cnt[r] = 0;
+  __syncthreads();
+  for (int i = tid; i < n; i += kPT) {
+    const int t = h[i];
+    if (t >= 0 && t < vocab) atomicOr(&bits[t >> 5], 1u << (t & 31));
+  }
+  __syncthreads();
+  // Exclusive prefix popcount over words, in chunks of kPT words.
+  uint32_t carry = 0;
+  for (int w0 = 0; w0 < words; w0 += kPT) {
+    const int w = w0 + tid;
+    const uint32_t c = w < words ? __popc(bits[w]) : 0u;
+    uint32_t inc = c;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+      uint32_t v = __shfl_up(inc, o, kWave);
+      if ((tid & (kWave - 1)) >= o) inc += v;
+    }
+    if ((tid & (kWave - 1)) == kWave - 1) wave_tot[tid / kWave] = inc;
+    __syncthreads();
+    uint32_t before = carry;
+    for (int k = 0; k < tid / kWave; ++k) before += wave_tot[k];
+    if (w < words) rank[w] = before + inc - c;
+    uint32_t total = 0;
+    for (int k = 0; k < kPT / kWave; ++k) total += wave_tot[k];
+    carry += total;
+    __syncthreads();
+  }
+  const uint32_t distinct = carry;
+  for (int i = tid; i < n; i += kPT) {
+    const int t = h[i];
+    if (t >= 0 && t < vocab) {
+      const uint32_t bit = 1u << (t & 31);
+      atomicAdd(&cnt[rank[t >> 5] + __popc(bits[t >> 5] & (bit - 1u))], 1u);
+    }
+  }
+  __syncthreads();
+  uint32_t* bo = bits_out + static_cast<int64_t>(b) * words_stride;
+  uint32_t* ro = rank_out + static_cast<int64_t>(b) * words_stride;
+  for (int w = tid; w < words; w += kPT) {
+    bo[w] = bits[w];
+    ro[w] = rank[w];
+  }
+  const float f = freq ? freq[b] : 0.f;
+  const float p = pres ? pres[b] : 0.f;
+  float* ao = add_out + static_cast<int64_t>(b) * add_stride;
+  for (uint32_t r = tid; r < distinct; r += kPT) {
+    float acc = 0.f;  // scatter_add_ of `f`, once per occurrence
+    for (uint32_t i = 0; i < cnt[r]; ++i) acc += f;
+    float a = 0.f - acc;  // additive tensor starts at zero, then sub_ frequency
+    a = a - p;            // then sub_ presence
+    ao[r] = a;
+  }
+  if (tid == 0 && distinct_out) distinct_out[b] = static_cast<int32_t>(distinct);
+}
+
+// In-place adjustment of [rows, V] logits: penalties then mask (true order),
+// or the verify-path quirk (penalty built on zeros, then added).
+template <typename T>
+__global__ __launch_bounds__(kPT) void adjust_logits_kernel(
+    T* __restrict__ logits, int64_t row_stride, int64_t vocab, int rows_per_request,
+    const uint32_t* __restrict__ pbits, const uint32_t* __restrict__ prank, int64_t pwords_stride,
+    const float* __restrict__ padd, int64_t padd_stride, const float* __restrict__ rep, int quirk,
+    const int32_t* __restrict__ mask, int64_t mask_stride, int mask_rows_per_request, int64_t mask_vocab) {
+  const int64_t row = blockIdx.y;
+  const int64_t b = row / rows_per_request;
+  rs::XForm f;
+  f.pbits = pbits ? pbits + b * pwords_stride : nullptr;
+  f.prank = pbits ? prank + b * pwords_stride : nullptr;
+  f.padd = pbits ? padd + b * padd_stride : nullptr;
+  f.rep = rep ? rep[b] : 1.f;
+  f.quirk = quirk;
+  const int64_t mrow = mask_rows_per_request > 1 ? b : row;
+  f.mbits = mask ? reinterpret_cast<const uint32_t*>(mask) + mrow * mask_stride : nullptr;
+  T* rp = logits + row * row_stride;
+  for (int64_t v = static_cast<int64_t>(blockIdx.x) * kPT + threadIdx.x; v < vocab; v += static_cast<int64_t>(gridDim.x) * kPT) {
+    float x = to_f32<T>(rp[v]);
+    rs::XForm g = f;
+    if (v >= mask_vocab) g.mbits = nullptr;  // columns beyond the mask width stay untouched
+    float y = rs::transform1(g, x, v);
+    if (y != x) rp[v] = from_f32<T>(y);
+  }
+}
+
+}  // namespace
+}  // namespace ls
+
+extern "C" int ls_penalty_tables(const int32_t* history, int64_t history_stride, const int32_t* history_lens,
+                                 int64_t batch, int32_t history_cap, int64_t vocab, const float* frequency,
+                                 const float* presence, uint32_t* bits, uint32_t* rank, int64_t words_stride,
+                                 float* add, int64_t add_stride, int32_t* distinct, void* stream) {
+  using namespace ls;
+  LS_CHECK(batch > 0 && vocab > 0 && history_cap >= 0, LS_ERR_SHAPE, "ls_penalty_tables: bad sizes");
+  const int64_t words = (vocab + 31) / 32;
+  LS_CHECK(words_stride >= words && add_stride >= history_cap, LS_ERR_SHAPE,
+           "ls_penalty_tables: table strides too small (words %lld, history %d)", (long long)words, history_cap);
+  LS_CHECK(history || history_cap == 0, LS_ERR_VALUE, "ls_penalty_tables: null history");
+  LS_CHECK(bits && rank && add, LS_ERR_VALUE, "ls_penalty_tables: null output");
+  const size_t lds = (2 * static_cast<size_t>(words) + static_cast<size_t>(history_cap)) * 4;
+  LS_CHECK(lds <= 64 * 1024, LS_ERR_SHAPE,
+           "ls_penalty_tables: vocab %lld with history %d exceeds the 64 KiB LDS budget",
+           (long long)vocab, history_cap);
+  penalty_tables_kernel<<<dim3(static_cast<unsigned>(batch)), kPT, lds, static_cast<hipStream_t>(stream)>>>(
+      history, history_stride, history_lens, history_cap, vocab, static_cast<int>(words), frequency, presence,
+      bits, rank, words_stride, add, add_stride, distinct);
+  LS_LAUNCH_CHECK();
+  return LS_OK;
+}
+
+extern "C" int ls_adjust_logits(void* logits, int32_t logits_dtype, int64_t row_stride, int64_t rows,
+                                int64_t vocab, int32_t rows_per_request, const uint32_t* pen_bits,
+                                const uint32_t* pen_rank, int64_t pen_words_stride, const float* pen_add,
+                                int64_t pen_add_stride, const float* repetition, int32_t verify_quirk,
+                                const int32_t* vocab_mask, int64_t mask_stride, int32_t mask_rows_per_request,
+                                int64_t mask_words, void* stream) {
+  using namespace ls;
+  LS_CHECK(rows > 0 && vocab > 0 && rows_per_request > 0 && rows % rows_per_request == 0, LS_ERR_SHAPE,
+           "ls_adjust_logits: rows must be a positive multiple of rows_per_request");
+  LS_CHECK(row_stride >= vocab, LS_ERR_SHAPE, "ls_adjust_logits: row stride < vocab");
+  LS_CHECK(rows <= 65535, LS_ERR_SHAPE, "ls_adjust_logits: at most 65535 rows per call");
+  LS_CHECK(!pen_bits || (pen_rank && pen_add), LS_ERR_VALUE, "ls_adjust_logits: incomplete penalty tables");
+  LS_CHECK(!vocab_mask || (mask_rows_per_request == 1 || mask_rows_per_request == rows_per_request),
+           LS_ERR_VALUE, "ls_adjust_logits: mask must be per row or per request");
+  LS_CHECK(!vocab_mask || (mask_words > 0 && mask_words * 32 >= 1 && mask_stride >= mask_words), LS_ERR_SHAPE,
+           "ls_adjust_logits: bad mask shape");
+  const int64_t mask_vocab = vocab_mask ? (mask_words * 32 < vocab ? mask_words * 32 : vocab) : vocab;
+  dim3 grid(static_cast<unsigned>((vocab + kPT * 8 - 1) / (kPT * 8)), static_cast<unsigned>(rows));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+#define LS_ADJ(T)                                                                                         \
+  adjust_logits_kernel<T><<<grid, kPT, 0, s>>>(static_cast<T*>(logits), row_stride, vocab, rows_per_request, \
+                                                pen_bits, pen_rank, pen_words_stride, pen_add, pen_add_stride, \
+                                                repetition, verify_quirk, vocab_mask, mask_stride,             \
+                                                mask_rows_per_request, mask_vocab)
+  if (logits_dtype == LS_F32) LS_ADJ(float);
+  else if (logits_dtype == LS_BF16) LS_ADJ(uint16_t);
+  else if (logits_dtype == LS_F16) LS_ADJ(__half);
+  else return fail(LS_ERR_DTYPE, "ls_adjust_logits: logits must be fp32, bf16 or fp16");
+#undef LS_ADJ
+  LS_LAUNCH_CHECK();
+  return LS_OK;
+}

@@ -1,0 +1,1160 @@
+// Stochastic (rejection-sampling) chain verification, fused over the whole
+// target block:
+//
+//   target_scan  grid (B*K rows) x S slices.  Streams every target row once
+//                (bf16 / fp16 / fp32, 16-byte loads), applies penalties and the
+//                vocabulary mask in registers, and determines the row's
+//                sampling support exactly: temperature, top-k (ties to the
+//                lowest index), top-p, min-p.  Writes a row record with the
+//                probability of the verified drafted token.
+//   draft_scan   grid B x S.  Computes the first rejection L of its request
+//                and, for rejected requests only, scans draft row L the same
+//                way to rebuild the draft distribution q there.
+//   resolve      grid B.  Residual max(p - q, 0) over the target support,
+//                1e-8 degenerate-mass fallback to p, inverse-CDF draw.
+//
+// Semantics follow vendor/sglang/python/sglang/srt/speculative/
+// dspark_components/kernels/accept_sampling.py:259-343 (single-q acceptance
+// with the q row rebuilt from the draft logits; unnormalised CDF
+// "first v with cumsum > u * total"), with the target distribution of
+// .../speculative/dflash_utils.py:743-810 plus min-p, and the draft-probs
+// ("dense q") acceptance of .../speculative/reject_sampling.py:5-156.
+#include "rowscan.h"
+
+namespace ls {
+namespace {
+using namespace rs;
+
+struct RowRec {
+  float m;        // max scaled logit of the row
+  float z;        // normaliser of the support
+  float p_cand;   // probability of the drafted token this row verifies
+  int n;          // support entries (-1: dense support)
+  int flags;
+  int pad;
+  uint64_t last;  // key of the last support entry
+};
+
+struct Args {
+  // target
+  const void* logits;
+  int64_t lrs;
+  const void* cand;
+  int64_t csb, csk;
+  int cfirst;
+  int64_t batch;
+  int width;
+  int64_t vocab;
+  const float* temps;
+  const int32_t* top_ks;
+  const float* top_ps;
+  const float* min_ps;
+  // penalties / mask
+  const uint32_t* pbits;
+  const uint32_t* prank;
+  int64_t pws;
+  const float* padd;
+  int64_t pas;
+  const float* prep;
+  int quirk;
+  const uint32_t* mask;
+  int64_t mrs;
+  int mask_per_request;
+  // draft
+  int q_mode;  // 0: sampled q + draft logits; 1: dense draft probabilities
+  const float* dtp;
+  int64_t dtp_sb;
+  const void* draft;
+  int64_t dsb, dsk;
+  const float* d_temps;
+  const int32_t* d_top_ks;
+  const float* d_top_ps;
+  const float* d_min_ps;
+  // randomness
+  const float* uni;
+  int64_t usb;
+  const float* funi;
+  // outputs
+  int32_t* accept;
+  int64_t* bonus;
+  float* p_cand_out;  // [B, K-1] or null
+  int32_t* status;    // [1] or null: OR of row flags that blocked a request
+  // workspace
+  uint32_t* cnt_t;    // [B*K]
+  uint32_t* cnt_d;    // [B]
+  RowRec* rec_t;      // [B*K]
+  int32_t* sidx_t;    // [B*K, kCap]
+  float* sp_t;        // [B*K, kCap]
+  RowRec* rec_d;      // [B]
+  int32_t* sidx_d;    // [B, kCap]
+  float* sp_d;        // [B, kCap]
+  uint64_t* pub_t;    // [B*K, kNBuf] slice hand-off (S_t > 1)
+  uint64_t* pubs_t;   // [B*K, S_t, 2]
+  uint64_t* pub_d;    // [B, kNBuf]
+  uint64_t* pubs_d;   // [B, S_d, 2]
+  int s_t, s_d;
+};
+
+__device__ __forceinline__ void atomic_put_u64(uint64_t* p, uint64_t v) {
+  uint64_t old = __hip_atomic_exchange(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  asm volatile("" ::"v"(old));
+}
+
+// ------------------------------------------------------------------ scan ---
+
+struct ScanOut {
+  float mx;   // running max of x (thread)
+  float mz;   // reference max of z (thread)
+  float z;    // sum exp((x - mz) / T) (thread)
+};
+
+// Compaction of an over-full candidate buffer (all threads; rare).
+__device__ __noinline__ void compact_slow(Shared& sh, int mode, int k, float t, float off_s) {
+  const int count = sh.count;
+  if (count > kNBuf) {
+    __syncthreads();
+    if (threadIdx.x == 0) { sh.overflow = 1; sh.tau_x = INFINITY; }
+    __syncthreads();
+    return;
+  }
+  if (mode == kModeTopK) {
+    const uint32_t thr = select_kth_s(sh, count, k);
+    compact_ge(sh, thr);
+    if (threadIdx.x == 0) {
+      if (sh.count > kNBHi) { sh.overflow = 1; sh.tau_x = INFINITY; }
+      else sh.tau_x = x_threshold(unordered_f32(thr), t);
+    }
+  } else {
+    const float wmx = unordered_f32(*reinterpret_cast<unsigned*>(&sh.wg_max_x));
+    compact_ge(sh, ordered_f32(wmx / t + off_s));
+    if (threadIdx.x == 0 && sh.count > kNBHi) { sh.overflow = 1; sh.tau_x = INFINITY; }
+  }
+  __syncthreads();
+}
+
+// One maintenance point (all threads, once per step): publish the running
+// maximum (filter mode), compact the buffer when over the trigger, and return
+// the append threshold to use until the next step.
+__device__ __forceinline__ float maintain(Shared& sh, int mode, int k, float t, float off_s, float mx_thread) {
+  if (mode == kModeFilter) {
+    const float wm = wave_max(mx_thread);
+    if ((threadIdx.x & (kWave - 1)) == 0) atomicMax(reinterpret_cast<unsigned*>(&sh.wg_max_x), ordered_f32(wm));
+  }
+  __syncthreads();
+  // Every thread reads the decision inputs before any thread appends again
+  // (second barrier), so all threads take the same branch below.
+  const int count = sh.count;
+  const int ovf = sh.overflow;
+  const float wmx = unordered_f32(*reinterpret_cast<unsigned*>(&sh.wg_max_x));
+  __syncthreads();
+  if (count > kNBHi && !ovf) compact_slow(sh, mode, k, t, off_s);
+  float tau = sh.tau_x;
+  if (mode == kModeFilter && !sh.overflow) tau = x_threshold(wmx / t + off_s, t);
+  return tau;
+}
+
+template <typename Tag, bool kVec>
+__device__ ScanOut scan_range(Shared& sh, const typename Tag::storage* row, int64_t b, int64_t e,
+                              const XForm& f, float t, int mode, int k, float off_s) {
+  using S = typename Tag::storage;
+  constexpr int P = Tag::kPerVec;
+  const bool need_z = mode != kModeTopK;
+  const float c2 = 1.4426950408889634f / t;
+  const float off_x = (mode == kModeFilter) ? off_s * t : -INFINITY;
+  const int tid = threadIdx.x;
+  ScanOut o{-FLT_MAX, -FLT_MAX, 0.f};
+  float tau = sh.tau_x;
+  const int64_t nvv = (e - b + P - 1) / P;        // virtual vectors in [b, e)
+  const int64_t nfull = kVec ? (e - b) / P : 0;    // vectors loadable with 16-byte loads
+  const int64_t steps = (nvv + kT - 1) / kT;
+  const uint4* vp = reinterpret_cast<const uint4*>(row + b);
+  // Four 16-byte loads in flight per thread, rotated through a ring.
+  uint4 r0 = {}, r1 = {}, r2 = {}, r3 = {};
+  if (tid < nfull) r0 = load16_stream(vp + tid);
+  if (kT + tid < nfull) r1 = load16_stream(vp + kT + tid);
+  if (2 * kT + tid < nfull) r2 = load16_stream(vp + 2 * kT + tid);
+  if (3 * kT + tid < nfull) r3 = load16_stream(vp + 3 * kT + tid);
+  for (int64_t st = 0; st < steps; ++st) {
+    const int64_t i = st * kT + tid;
+    const uint4 cur = r0;
+    r0 = r1;
+    r1 = r2;
+    r2 = r3;
+    const int64_t inext = i + 4 * kT;
+    if (inext < nfull) r3 = load16_stream(vp + inext);
+    float x[P];
+    if (i < nfull) {
+      unpack16<Tag>(cur, x);
+    } else {
+#pragma unroll
+      for (int q = 0; q < P; ++q) {
+        const int64_t v = b + i * P + q;
+        x[q] = (i < nvv && v < e) ? to_f32<S>(row[v]) : -INFINITY;
+      }
+    }
+    const int64_t e0 = b + i * P;
+    if (i < nvv && (f.pbits || f.mbits)) {
+      if (i < nfull) {
+        transform_vec<P>(f, x, e0);
+      } else {
+#pragma unroll
+        for (int q = 0; q < P; ++q)
+          if (e0 + q < e) x[q] = transform1(f, x[q], e0 + q);
+      }
+    }
+    float vmax = x[0];
+#pragma unroll
+    for (int q = 1; q < P; ++q) vmax = fmaxf(vmax, x[q]);
+    if (need_z) {
+      if (vmax > o.mz) {
+        o.z *= __builtin_amdgcn_exp2f((o.mz - vmax) * c2);
+        o.mz = vmax;
+      }
+#pragma unroll
+      for (int q = 0; q < P; ++q) o.z += __builtin_amdgcn_exp2f((x[q] - o.mz) * c2);
+    }
+    o.mx = fmaxf(o.mx, vmax);
+    const float tau_eff = fmaxf(tau, o.mx + off_x);
+    if (__ballot(vmax >= tau_eff)) append_vec<P>(sh, x, tau_eff, e0, t);
+    tau = maintain(sh, mode, k, t, off_s, o.mx);
+  }
+  return o;
+}
+
+// After the scan of a slice: final compaction of the slice's candidates and
+// workgroup-wide statistics.  Returns (max x, reference max, z).
+__device__ __noinline__ ScanOut finish_slice(Shared& sh, const ScanOut& o, int mode, int k, float t, float off_s) {
+  ScanOut r;
+  r.mx = block_max(sh, o.mx);
+  if (mode != kModeTopK) {
+    const float gm = r.mx;
+    float zt = (o.mz == -FLT_MAX) ? 0.f : o.z * __builtin_amdgcn_exp2f((o.mz - gm) * (1.4426950408889634f / t));
+    r.z = block_sum(sh, zt);
+    r.mz = gm;
+  } else {
+    r.z = 0.f;
+    r.mz = r.mx;
+  }
+  if (!sh.overflow) {
+    const int count = sh.count;
+    if (mode == kModeTopK && count > k) {
+      const uint32_t thr = select_kth_s(sh, count, k);
+      compact_ge(sh, thr);
+    } else if (mode == kModeFilter && count > 0) {
+      compact_ge(sh, ordered_f32(r.mx / t + off_s));
+    }
+  }
+  __syncthreads();
+  return r;
+}
+
+// --------------------------------------------------------------- finalise ---
+
+// Index of the first entry i < n (entries sorted by key, e_i = exp(s_i - m))
+// at which the running sum before i, divided by `denom`, exceeds `limit`;
+// n if none.  Also returns the full sum of e_i / denom through *total.
+__device__ __noinline__ int first_excl_exceeds(Shared& sh, int n, float m, float denom, float limit, float* total) {
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1), wid = tid / kWave;
+  __shared__ int found;
+  __shared__ float wsum[kT / kWave];
+  if (tid == 0) found = n;
+  float carry = 0.f;
+  __syncthreads();
+  for (int r = 0; r < n; r += kT) {
+    const int i = r + tid;
+    const float p = i < n ? __expf(key_s(sh.buf[i]) - m) / denom : 0.f;
+    float inc = p;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+      float v = __shfl_up(inc, o, kWave);
+      if (lane >= o) inc += v;
+    }
+    if (lane == kWave - 1) wsum[wid] = inc;
+    __syncthreads();
+    float before = carry;
+    for (int w = 0; w < wid; ++w) before += wsum[w];
+    const float excl = before + inc - p;
+    if (i < n && excl > limit) atomicMin(&found, i);
+    float tot = 0.f;
+    for (int w = 0; w < kT / kWave; ++w) tot += wsum[w];
+    carry += tot;
+    __syncthreads();
+    const int f = found;
+    __syncthreads();  // all threads have read `found` before any thread updates it again
+    if (f < n) break;
+  }
+  if (total) *total = carry;
+  const int res = found;
+  __syncthreads();
+  return res;
+}
+
+// ------------------------------------------------------- exact fallback ---
+//
+// Used when the candidate buffer cannot hold a row's support (heavy ties at
+// the top-k value, top-k above the buffer capacity, a top-p nucleus that is
+// not closed by the candidates).  One workgroup re-reads the row from global
+// memory several times and selects the exact cut keys by MSB-first radix
+// select over the 64-bit candidate keys (8-bit digits): by count for top-k,
+// by mass exp(s - m) for top-p, and by value for min-p.
+
+struct Hist {
+  uint32_t cnt[256];
+  float mass[256];
+};
+
+// One pass over the row: histogram of digit (key >> shift) & 255 of every key
+// >= kmin whose bits under pmask equal prefix (counts and masses).
+template <typename Tag>
+__device__ __noinline__ void hist_pass(Hist& h, const typename Tag::storage* row, int64_t vocab, const XForm& f,
+                                       float t, float m, uint64_t kmin, uint64_t prefix, uint64_t pmask, int shift) {
+  const int tid = threadIdx.x;
+  h.cnt[tid] = 0;
+  h.mass[tid] = 0.f;
+  __syncthreads();
+  for (int64_t v = tid; v < vocab; v += kT) {
+    const float s = transform1(f, to_f32<typename Tag::storage>(row[v]), v) / t;
+    const uint64_t key = cand_key(s, static_cast<int>(v));
+    if (key >= kmin && (key & pmask) == prefix) {
+      const int d = static_cast<int>((key >> shift) & 255u);
+      atomicAdd(&h.cnt[d], 1u);
+      atomicAdd(&h.mass[d], __expf(s - m));
+    }
+  }
+  __syncthreads();
+}
+
+// k-th largest key of the row (k >= 1).
+template <typename Tag>
+__device__ __noinline__ uint64_t select_key_by_count(Hist& h, const typename Tag::storage* row, int64_t vocab,
+                                                     const XForm& f, float t, float m, int k) {
+  __shared__ int s_d, s_above;
+  uint64_t prefix = 0, pmask = 0;
+  int remaining = k;
+  for (int shift = 56; shift >= 0; shift -= 8) {
+    hist_pass<Tag>(h, row, vocab, f, t, m, 0, prefix, pmask, shift);
+    if (threadIdx.x == 0) {
+      int above = 0, d = 0;
+      for (d = 255; d > 0; --d) {
+        if (above + static_cast<int>(h.cnt[d]) >= remaining) break;
+        above += static_cast<int>(h.cnt[d]);
+      }
+      s_d = d;
+      s_above = above;
+    }
+    __syncthreads();
+    prefix |= static_cast<uint64_t>(s_d) << shift;
+    pmask |= uint64_t(255) << shift;
+    remaining -= s_above;
+    __syncthreads();
+  }
+  return prefix;
+}
+
+// Smallest key K >= kmin whose excluded mass (sum of exp(s - m) over keys
+// > K and >= kmin) is <= limit: the last entry a top-p cut keeps.
+template <typename Tag>
+__device__ __noinline__ uint64_t select_key_by_mass(Hist& h, const typename Tag::storage* row, int64_t vocab,
+                                                    const XForm& f, float t, float m, uint64_t kmin, float limit) {
+  __shared__ int s_d;
+  __shared__ float s_above;
+  uint64_t prefix = 0, pmask = 0;
+  float above = 0.f;
+  for (int shift = 56; shift >= 0; shift -= 8) {
+    hist_pass<Tag>(h, row, vocab, f, t, m, kmin, prefix, pmask, shift);
+    if (threadIdx.x == 0) {
+      float cum = above, sel_above = above;
+      int sel = -1;
+      for (int d = 255; d >= 0; --d) {
+        if (h.cnt[d] == 0) continue;
+        if (cum <= limit) {
+          sel = d;
+          sel_above = cum;
+        } else {
+          break;
+        }
+        cum += h.mass[d];
+      }
+      s_d = sel < 0 ? 0 : sel;
+      s_above = sel_above;
+    }
+    __syncthreads();
+    prefix |= static_cast<uint64_t>(s_d) << shift;
+    pmask |= uint64_t(255) << shift;
+    above = s_above;
+    __syncthreads();
+  }
+  return prefix;
+}
+
+// Count and mass of keys >= kmin; optionally the smallest s among keys >=
+// kmin with exp(s - m) >= emin (as an ordered value, 0xffffffff if none).
+template <typename Tag>
+__device__ __noinline__ void tally(Shared& sh, const typename Tag::storage* row, int64_t vocab, const XForm& f, float t,
+                                   float m, uint64_t kmin, float emin, int* count, float* mass, uint32_t* smin_ord) {
+  __shared__ unsigned s_cnt, s_min;
+  const int tid = threadIdx.x;
+  if (tid == 0) { s_cnt = 0; s_min = 0xffffffffu; }
+  __syncthreads();
+  float acc = 0.f;
+  unsigned c = 0, mn = 0xffffffffu;
+  for (int64_t v = tid; v < vocab; v += kT) {
+    const float s = transform1(f, to_f32<typename Tag::storage>(row[v]), v) / t;
+    const uint64_t key = cand_key(s, static_cast<int>(v));
+    if (key >= kmin) {
+      const float e = __expf(s - m);
+      acc += e;
+      ++c;
+      if (e >= emin) mn = min(mn, static_cast<unsigned>(key >> 32));
+    }
+  }
+  atomicAdd(&s_cnt, c);
+  atomicMin(&s_min, mn);
+  const float tot = block_sum(sh, acc);
+  *count = static_cast<int>(s_cnt);
+  *mass = tot;
+  *smin_ord = s_min;
+  __syncthreads();
+}
+
+// Collect every key >= kmin into sh.buf (at most kNBuf entries), sorted descending.
+template <typename Tag>
+__device__ __noinline__ int collect(Shared& sh, const typename Tag::storage* row, int64_t vocab, const XForm& f,
+                                    float t, uint64_t kmin) {
+  if (threadIdx.x == 0) sh.count = 0;
+  __syncthreads();
+  for (int64_t v = threadIdx.x; v < vocab; v += kT) {
+    const float s = transform1(f, to_f32<typename Tag::storage>(row[v]), v) / t;
+    const uint64_t key = cand_key(s, static_cast<int>(v));
+    if (key >= kmin) {
+      const int pos = atomicAdd(&sh.count, 1);
+      if (pos < kNBuf) sh.buf[pos] = key;
+    }
+  }
+  __syncthreads();
+  const int n = min(sh.count, 2048);
+  sort_desc(sh, n);
+  return n;
+}
+
+struct Exact {
+  float m, z;
+  uint64_t kcut;  // support = keys >= kcut
+  int n;          // support size
+};
+
+// Exact support of a row from global memory.  m_x: row max of x; z_dense:
+// sum over the row of exp(s - m) (filter / dense modes).
+template <typename Tag>
+__device__ __noinline__ Exact exact_support(Shared& sh, const typename Tag::storage* row, int64_t vocab,
+                                            const XForm& f, const Params& p, int mode, float m_x, float z_dense) {
+  __shared__ Hist h;
+  const float t = p.temperature;
+  Exact r;
+  r.m = m_x / t;
+  uint64_t kmin = 0;
+  float z1 = z_dense;
+  int cnt;
+  float mass;
+  uint32_t smin;
+  if (mode == kModeTopK && p.top_k < vocab) {
+    kmin = select_key_by_count<Tag>(h, row, vocab, f, t, r.m, p.top_k);
+    tally<Tag>(sh, row, vocab, f, t, r.m, kmin, INFINITY, &cnt, &z1, &smin);
+  }
+  uint64_t kcut = kmin;
+  if (p.top_p < 1.0f) kcut = select_key_by_mass<Tag>(h, row, vocab, f, t, r.m, kmin, p.top_p * z1);
+  if (p.min_p > 0.f) {
+    // Over the top-p set: p2 = (e / z1) / P with P its mass; drop p2 < p2_max * min_p.
+    tally<Tag>(sh, row, vocab, f, t, r.m, kcut, INFINITY, &cnt, &mass, &smin);
+    const float pp = mass / z1;
+    const float thr = ((1.0f / z1) / pp) * p.min_p;
+    // keep e with (e / z1) / pp >= thr: find the smallest such s
+    float emin = thr * pp * z1;
+    tally<Tag>(sh, row, vocab, f, t, r.m, kcut, emin, &cnt, &mass, &smin);
+    if (smin != 0xffffffffu) {
+      const uint64_t kmp = static_cast<uint64_t>(smin) << 32;
+      if (kmp > kcut) kcut = kmp;
+    }
+  }
+  tally<Tag>(sh, row, vocab, f, t, r.m, kcut, INFINITY, &cnt, &mass, &smin);
+  r.z = mass;
+  r.kcut = kcut;
+  r.n = cnt;
+  return r;
+}
+
+// Determine the exact support from the candidate buffer (or, if it could not
+// hold the support, from the row itself) and write the row record.  `cand_x`
+// is the transformed logit of the drafted token this row verifies.  All
+// threads.
+template <typename Tag>
+__device__ __noinline__ void finalize_row(Shared& sh, const ScanOut& st, const Params& p, int mode, int64_t vocab,
+                                          const typename Tag::storage* row, const XForm& f, RowRec* rec,
+                                          int32_t* sidx, float* sp, int cand_tok, float cand_x) {
+  const int tid = threadIdx.x;
+  __shared__ float s_m, s_z;
+  __shared__ int s_n, s_flags;
+  __shared__ uint64_t s_last;
+  const float t = p.temperature;
+  if (tid == 0) {
+    s_flags = sh.overflow ? kFlagOverflow : 0;
+    s_last = 0;
+  }
+  __syncthreads();
+  int n = sh.count;
+  if (mode == kModeDense) {
+    if (tid == 0) {
+      s_m = st.mx / t;
+      s_z = st.z;
+      s_n = -1;
+      s_flags |= kFlagDense;
+    }
+  } else if (!s_flags) {
+    if (n > 2048) {
+      if (tid == 0) s_flags |= kFlagOverflow;
+    } else {
+      sort_desc(sh, n);
+      if (mode == kModeTopK && n > p.top_k) n = p.top_k;
+      const float m = n > 0 ? key_s(sh.buf[0]) : -INFINITY;
+      float z1;
+      if (mode == kModeTopK) {
+        float acc = 0.f;
+        for (int i = tid; i < n; i += kT) acc += __expf(key_s(sh.buf[i]) - m);
+        z1 = block_sum(sh, acc);
+      } else {
+        z1 = st.z;  // dense normaliser relative to the row maximum
+      }
+      int n_f = n;
+      float mass_all = 0.f;
+      if (p.top_p < 1.0f && n > 0) {
+        n_f = first_excl_exceeds(sh, n, m, z1, p.top_p, &mass_all);
+        if (mode == kModeFilter && p.min_p <= 0.f && n_f == n && mass_all <= p.top_p) {
+          if (tid == 0) s_flags |= kFlagOverflow;  // nucleus extends past the candidates
+        }
+      }
+      if (p.min_p > 0.f && n_f > 0) {
+        // Renormalise over the top-p prefix, then drop p < p_max * min_p.
+        float acc = 0.f;
+        for (int i = tid; i < n_f; i += kT) acc += __expf(key_s(sh.buf[i]) - m) / z1;
+        const float pp = block_sum(sh, acc);
+        const float p0 = (__expf(key_s(sh.buf[0]) - m) / z1) / pp;
+        const float thr = p0 * p.min_p;
+        __shared__ int cut;
+        if (tid == 0) cut = n_f;
+        __syncthreads();
+        for (int i = tid; i < n_f; i += kT) {
+          const float pi = (__expf(key_s(sh.buf[i]) - m) / z1) / pp;
+          if (pi < thr) atomicMin(&cut, i);
+        }
+        __syncthreads();
+        n_f = cut;
+        __syncthreads();
+      }
+      if (n_f > kCap && tid == 0) s_flags |= kFlagOverflow;
+      float acc = 0.f;
+      for (int i = tid; i < n_f; i += kT) acc += __expf(key_s(sh.buf[i]) - m);
+      const float zf = block_sum(sh, acc);
+      if (tid == 0) {
+        s_m = m;
+        s_z = zf;
+        s_n = n_f;
+        s_last = n_f > 0 ? sh.buf[n_f - 1] : ~uint64_t(0);
+      }
+      __syncthreads();
+    }
+  }
+  __syncthreads();
+  if (s_flags & kFlagOverflow) {
+    // Exact fallback from global memory.
+    const Exact ex = exact_support<Tag>(sh, row, vocab, f, p, mode, st.mx, st.z);
+    int n_f = ex.n;
+    if (n_f <= kCap) n_f = collect<Tag>(sh, row, vocab, f, t, ex.kcut);
+    if (tid == 0) {
+      s_m = ex.m;
+      s_z = ex.z;
+      s_flags = 0;
+      if (ex.n <= kCap && n_f == ex.n) {
+        s_n = n_f;
+        s_last = n_f > 0 ? sh.buf[n_f - 1] : ~uint64_t(0);
+      } else {
+        s_n = -1;  // threshold support evaluated densely
+        s_last = ex.kcut;
+        s_flags = kFlagDense;
+      }
+    }
+    __syncthreads();
+  }
+  if (s_n > 0) {
+    for (int i = tid; i < s_n; i += kT) {
+      const uint64_t kk = sh.buf[i];
+      sidx[i] = key_idx(kk);
+      sp[i] = __expf(key_s(kk) - s_m) / s_z;
+    }
+  }
+  __syncthreads();
+  if (tid == 0) {
+    RowRec r;
+    r.m = s_m;
+    r.z = s_z;
+    r.n = s_n;
+    r.flags = s_flags;
+    r.pad = 0;
+    r.last = s_last;
+    r.p_cand = 0.f;
+    if (cand_tok >= 0) {
+      const float sc = cand_x / t;
+      const uint64_t kc = cand_key(sc, cand_tok);
+      r.p_cand = (kc >= r.last && (r.n != 0 || (r.flags & kFlagDense))) ? __expf(sc - r.m) / r.z : 0.f;
+    }
+    *rec = r;
+  }
+  __syncthreads();
+}
+
+// ------------------------------------------------------- slice hand-off ---
+
+// Publish this slice's candidates and statistics, arrive on the row counter,
+// and, in the last slice to arrive, gather all slices into LDS.  Returns true
+// in the workgroup that continues with the row.
+__device__ __noinline__ bool merge_slices(Shared& sh, ScanOut& st, int mode, int slices, int slice, uint64_t* pub,
+                             uint64_t* pubs, uint32_t* counter, float t) {
+  const int tid = threadIdx.x;
+  __shared__ int is_last;
+  const int cap = kNBuf / slices;
+  const int n = sh.count;
+  const bool ovf = sh.overflow || n > cap;
+  uint64_t* my = pub + static_cast<int64_t>(slice) * cap;
+  if (!ovf)
+    for (int i = tid; i < n; i += kT) atomic_put_u64(my + i, sh.buf[i]);
+  if (tid == 0) {
+    atomic_put_u64(pubs + 2 * slice, ovf ? ~uint64_t(0) : static_cast<uint64_t>(n));
+    atomic_put_u64(pubs + 2 * slice + 1,
+                   (static_cast<uint64_t>(ordered_f32(st.mx)) << 32) | __float_as_uint(st.z));
+  }
+  __syncthreads();  // every thread's publishes have completed
+  if (tid == 0) is_last = (arrive(counter) == static_cast<uint32_t>(slices - 1));
+  __syncthreads();
+  if (!is_last) return false;
+  __shared__ int offs[17];
+  __shared__ float smx[16], sz[16];
+  if (tid == 0) {
+    atomic_take_u32(counter);
+    int total = 0, bad = 0;
+    for (int s = 0; s < slices; ++s) {
+      const uint64_t c = atomic_take_u64(pubs + 2 * s);
+      const uint64_t mz = atomic_take_u64(pubs + 2 * s + 1);
+      offs[s] = total;
+      if (c == ~uint64_t(0)) bad = 1;
+      else total += static_cast<int>(c);
+      smx[s] = unordered_f32(static_cast<uint32_t>(mz >> 32));
+      sz[s] = __uint_as_float(static_cast<uint32_t>(mz));
+    }
+    offs[slices] = total;
+    sh.overflow = bad || total > kNBuf;
+    sh.count = sh.overflow ? 0 : total;
+    float gm = -FLT_MAX, z = 0.f;
+    for (int s = 0; s < slices; ++s) gm = fmaxf(gm, smx[s]);
+    if (mode != kModeTopK) {
+      const float c2 = 1.4426950408889634f / t;
+      for (int s = 0; s < slices; ++s)
+        if (smx[s] != -FLT_MAX) z += sz[s] * __builtin_amdgcn_exp2f((smx[s] - gm) * c2);
+    }
+    smx[0] = gm;
+    sz[0] = z;
+  }
+  __syncthreads();
+  st.mx = smx[0];
+  st.mz = smx[0];
+  st.z = sz[0];
+  if (!sh.overflow) {
+    for (int s = 0; s < slices; ++s) {
+      const int base = offs[s], cnt = offs[s + 1] - offs[s];
+      for (int i = tid; i < cnt; i += kT) sh.buf[base + i] = atomic_take_u64(pub + static_cast<int64_t>(s) * cap + i);
+    }
+  }
+  __syncthreads();
+  return true;
+}
+
+__device__ void init_shared(Shared& sh, int mode) {
+  if (threadIdx.x == 0) {
+    sh.count = 0;
+    sh.overflow = 0;
+    sh.tau_x = (mode == kModeDense) ? INFINITY : -FLT_MAX;
+    *reinterpret_cast<unsigned*>(&sh.wg_max_x) = ordered_f32(-FLT_MAX);
+  }
+  __syncthreads();
+}
+
+__device__ __forceinline__ float filter_offset(const Params& p) {
+  // scaled-logit offset below the running max that can still be in the support
+  if (p.min_p > 0.f) return __logf(p.min_p) - 1e-3f;
+  return -kDeltaTopP;
+}
+
+__device__ __forceinline__ int slices_clamped(int s, int64_t vocab) { return s; }
+
+template <typename Tag, bool kVec>
+__device__ void process_row(Shared& sh, const typename Tag::storage* row, int64_t vocab, const Params& p,
+                            const XForm& f, int slices, int slice, uint64_t* pub, uint64_t* pubs, uint32_t* cnt,
+                            RowRec* rec, int32_t* sidx, float* sp, int cand_tok, float cand_x) {
+  const int mode = row_mode(p, vocab);
+  init_shared(sh, mode);
+  const int k = mode == kModeTopK ? max(p.top_k, 1) : 0;
+  const float off_s = mode == kModeFilter ? filter_offset(p) : 0.f;
+  const SliceRange r = slice_range(vocab, slices, slice, Tag::kPerVec);
+  ScanOut o = scan_range<Tag, kVec>(sh, row, r.v_begin, r.v_end, f, p.temperature, mode, k, off_s);
+  ScanOut st = finish_slice(sh, o, mode, k, p.temperature, off_s);
+  if (slices > 1) {
+    if (!merge_slices(sh, st, mode, slices, slice, pub, pubs, cnt, p.temperature)) return;
+    if (!sh.overflow) {
+      // re-apply the row-wide thresholds to the merged candidates
+      if (mode == kModeTopK && sh.count > k) compact_ge(sh, select_kth_s(sh, sh.count, k));
+      else if (mode == kModeFilter) compact_ge(sh, ordered_f32(st.mx / p.temperature + off_s));
+    }
+  }
+  finalize_row<Tag>(sh, st, p, mode, vocab, row, f, rec, sidx, sp, cand_tok, cand_x);
+}
+
+template <typename CandT>
+__device__ __forceinline__ int64_t cand_at(const Args& a, int64_t b, int j) {
+  return static_cast<int64_t>(static_cast<const CandT*>(a.cand)[b * a.csb + static_cast<int64_t>(a.cfirst + j) * a.csk]);
+}
+
+__device__ __forceinline__ XForm target_xform(const Args& a, int64_t b, int64_t row) {
+  XForm f;
+  f.pbits = a.pbits ? a.pbits + b * a.pws : nullptr;
+  f.prank = a.pbits ? a.prank + b * a.pws : nullptr;
+  f.padd = a.pbits ? a.padd + b * a.pas : nullptr;
+  f.rep = a.prep ? a.prep[b] : 1.f;
+  f.quirk = a.quirk;
+  f.mbits = a.mask ? a.mask + (a.mask_per_request ? b : row) * a.mrs : nullptr;
+  return f;
+}
+
+// --------------------------------------------------------------- kernels ---
+
+template <typename TagT, bool kVec, typename CandT>
+__global__ __launch_bounds__(kT) void target_scan_kernel(Args a) {
+  __shared__ Shared sh;
+  const int64_t row = blockIdx.x / a.s_t;
+  const int slice = blockIdx.x % a.s_t;
+  const int64_t b = row / a.width;
+  const int j = static_cast<int>(row % a.width);
+  Params p{a.temps[b], a.top_ks ? max(a.top_ks[b], 1) : static_cast<int>(a.vocab), a.top_ps ? a.top_ps[b] : 1.f,
+           a.min_ps ? a.min_ps[b] : 0.f};
+  using S = typename TagT::storage;
+  const S* rp = static_cast<const S*>(a.logits) + row * a.lrs;
+  const XForm f = target_xform(a, b, row);
+  int cand_tok = -1;
+  float cand_x = NAN;
+  if (j < a.width - 1) {
+    const int64_t c = cand_at<CandT>(a, b, j);
+    if (c >= 0 && c < a.vocab) {
+      cand_tok = static_cast<int>(c);
+      cand_x = transform1(f, to_f32<S>(rp[c]), c);
+    }
+  }
+  process_row<TagT, kVec>(sh, rp, a.vocab, p, f, a.s_t, slice, a.pub_t + row * kNBuf,
+                          a.pubs_t + row * a.s_t * 2, a.cnt_t + row, a.rec_t + row,
+                          a.sidx_t + row * kCap, a.sp_t + row * kCap, cand_tok, cand_x);
+}
+
+// First rejected position of request b (width-1 when every drafted token is
+// accepted), from the target row records.  Also reports blocking flags.
+template <typename CandT>
+__device__ int accept_length(const Args& a, int64_t b, int* flags) {
+  const int g = a.width - 1;
+  int len = 0;
+  *flags = 0;
+  for (; len < g; ++len) {
+    const RowRec& r = a.rec_t[b * a.width + len];
+    if (r.flags & kFlagOverflow) { *flags = r.flags; return len; }
+    float q;
+    if (a.q_mode == 0) {
+      q = a.dtp[b * a.dtp_sb + len];
+    } else {
+      const int64_t c = cand_at<CandT>(a, b, len);
+      q = (c >= 0 && c < a.vocab)
+              ? static_cast<const float*>(a.draft)[b * a.dsb + static_cast<int64_t>(len) * a.dsk + c]
+              : 0.f;
+    }
+    const float u = a.uni[b * a.usb + len];
+    if (!(u * q < r.p_cand)) break;
+  }
+  if (a.rec_t[b * a.width + len].flags & kFlagOverflow) *flags = kFlagOverflow;
+  return len;
+}
+
+template <typename TagD, bool kVec, typename CandT>
+__global__ __launch_bounds__(kT) void draft_scan_kernel(Args a) {
+  __shared__ Shared sh;
+  __shared__ int s_len, s_flags;
+  const int64_t b = blockIdx.x / a.s_d;
+  const int slice = blockIdx.x % a.s_d;
+  if (threadIdx.x == 0) s_len = accept_length<CandT>(a, b, &s_flags);
+  __syncthreads();
+  const int len = s_len;
+  if (len >= a.width - 1 || s_flags) {
+    if (slice == 0 && threadIdx.x == 0) {
+      RowRec r{};
+      r.flags = kFlagSkip;
+      a.rec_d[b] = r;
+    }
+    return;
+  }
+  Params p;
+  p.temperature = a.d_temps ? a.d_temps[b] : a.temps[b];
+  p.top_k = a.d_top_ks ? max(a.d_top_ks[b], 1) : static_cast<int>(a.vocab);
+  p.top_p = a.d_top_ps ? a.d_top_ps[b] : 1.f;
+  p.min_p = a.d_min_ps ? a.d_min_ps[b] : 0.f;
+  using S = typename TagD::storage;
+  const S* rp = static_cast<const S*>(a.draft) + b * a.dsb + static_cast<int64_t>(len) * a.dsk;
+  XForm f{nullptr, nullptr, nullptr, 1.f, 0, nullptr};
+  process_row<TagD, kVec>(sh, rp, a.vocab, p, f, a.s_d, slice, a.pub_d + b * kNBuf, a.pubs_d + b * a.s_d * 2,
+                          a.cnt_d + b, a.rec_d + b, a.sidx_d + b * kCap, a.sp_d + b * kCap, -1, NAN);
+}
+
+// Probability of token v under the target row record (dense supports only).
+template <typename TagT>
+__device__ __forceinline__ float target_p_dense(const Args& a, const RowRec& r, int64_t b, int64_t row, int64_t v,
+                                                const XForm& f, float t) {
+  using S = typename TagT::storage;
+  const float s = transform1(f, to_f32<S>(static_cast<const S*>(a.logits)[row * a.lrs + v]), v) / t;
+  if (r.last != 0 && cand_key(s, static_cast<int>(v)) < r.last) return 0.f;
+  return __expf(s - r.m) / r.z;
+}
+
+template <typename TagD>
+__device__ __forceinline__ float draft_q(const Args& a, const RowRec& d, const uint64_t* dsorted, int dn, int64_t b,
+                                         int len, int64_t v, float td) {
+  if (a.q_mode == 1) return static_cast<const float*>(a.draft)[b * a.dsb + static_cast<int64_t>(len) * a.dsk + v];
+  if (d.flags & kFlagDense) {
+    using S = typename TagD::storage;
+    const float s = to_f32<S>(static_cast<const S*>(a.draft)[b * a.dsb + static_cast<int64_t>(len) * a.dsk + v]) / td;
+    if (d.last != 0 && cand_key(s, static_cast<int>(v)) < d.last) return 0.f;
+    return __expf(s - d.m) / d.z;
+  }
+  // binary search in the draft support sorted by ascending index
+  int lo = 0, hi = dn - 1;
+  const uint32_t want = 0xffffffffu - static_cast<uint32_t>(v);
+  while (lo <= hi) {
+    const int mid = (lo + hi) >> 1;
+    const uint32_t kidx = static_cast<uint32_t>(dsorted[mid] >> 32);
+    if (kidx == want) return __uint_as_float(static_cast<uint32_t>(dsorted[mid]));
+    if (kidx > want) lo = mid + 1;  // larger (0xffffffff - idx) = smaller idx: entries are descending
+    else hi = mid - 1;
+  }
+  return 0.f;
+}
+
+// Sort (idx, p) pairs by ascending index into sh.buf[base ..): key =
+// (0xffffffff - idx) << 32 | bits(p), sorted descending.
+__device__ void load_sorted_by_index(Shared& sh, uint64_t* dst, const int32_t* idx, const float* pv, int n) {
+  for (int i = threadIdx.x; i < n; i += kT)
+    dst[i] = (static_cast<uint64_t>(0xffffffffu - static_cast<uint32_t>(idx[i])) << 32) | __float_as_uint(pv[i]);
+  __syncthreads();
+  // bitonic sort of dst[0..n) (n <= kCap), padded with zeros
+  int np = 1;
+  while (np < n) np <<= 1;
+  for (int i = n + threadIdx.x; i < np; i += kT) dst[i] = 0;
+  __syncthreads();
+  for (int size = 2; size <= np; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int i = threadIdx.x; i < np / 2; i += kT) {
+        const int lo = 2 * i - (i & (stride - 1));
+        const int hi = lo + stride;
+        const bool desc = ((lo & size) == 0);
+        const uint64_t x = dst[lo], y = dst[hi];
+        if ((x < y) == desc) { dst[lo] = y; dst[hi] = x; }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// Inverse-CDF draw over values val(i), i < n, in order: first i whose running
+// sum exceeds u * total (total = full running sum); returns i or -1.
+template <typename F>
+__device__ int cdf_find(Shared& sh, int n, float u, F val, float total) {
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1), wid = tid / kWave;
+  __shared__ int found;
+  __shared__ float wsum[kT / kWave];
+  if (tid == 0) found = -1;
+  const float thr = u * total;
+  float carry = 0.f;
+  __syncthreads();
+  for (int r = 0; r < n; r += kT) {
+    const int i = r + tid;
+    const float v = i < n ? val(i) : 0.f;
+    float inc = v;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+      float w = __shfl_up(inc, o, kWave);
+      if (lane >= o) inc += w;
+    }
+    if (lane == kWave - 1) wsum[wid] = inc;
+    __syncthreads();
+    float before = carry;
+    for (int w = 0; w < wid; ++w) before += wsum[w];
+    if (i < n && before + inc > thr) atomicMin(reinterpret_cast<unsigned*>(&found), static_cast<unsigned>(i));
+    float tot = 0.f;
+    for (int w = 0; w < kT / kWave; ++w) tot += wsum[w];
+    carry += tot;
+    __syncthreads();
+    const int f = found;
+    __syncthreads();  // all threads have read `found` before any thread updates it again
+    if (f >= 0) break;
+  }
+  const int res = found;
+  __syncthreads();
+  return res;
+}
+
+template <typename TagT, typename TagD, typename CandT>
+__global__ __launch_bounds__(kT) void resolve_kernel(Args a) {
+  __shared__ Shared sh;
+  __shared__ int s_len, s_flags, s_tok;
+  __shared__ float s_mass, s_total;
+  const int64_t b = blockIdx.x;
+  const int tid = threadIdx.x;
+  if (tid == 0) s_len = accept_length<CandT>(a, b, &s_flags);
+  __syncthreads();
+  const int len = s_len;
+  const int g = a.width - 1;
+  if (a.p_cand_out)
+    for (int j = tid; j < g; j += kT) a.p_cand_out[b * g + j] = a.rec_t[b * a.width + j].p_cand;
+  const int64_t trow = b * a.width + len;
+  const RowRec tr = a.rec_t[trow];
+  const bool rejected = len < g;
+  RowRec dr{};
+  if (rejected && a.q_mode == 0) dr = a.rec_d[b];
+  const bool blocked = s_flags || (tr.flags & kFlagOverflow) ||
+                       (rejected && a.q_mode == 0 && (dr.flags & (kFlagOverflow | kFlagSkip)));
+  if (blocked) {
+    if (tid == 0) {
+      a.accept[b] = -1;
+      a.bonus[b] = -1;
+      if (a.status) atomicOr(a.status, kFlagOverflow);
+    }
+    return;
+  }
+  const float td = a.d_temps ? a.d_temps[b] : a.temps[b];
+  // Draft support sorted by index (sparse q rows only) in the upper LDS half.
+  uint64_t* dsorted = sh.buf + 2048;
+  int dn = 0;
+  if (rejected && a.q_mode == 0 && !(dr.flags & kFlagDense)) {
+    dn = dr.n;
+    load_sorted_by_index(sh, dsorted, a.sidx_d + b * kCap, a.sp_d + b * kCap, dn);
+  }
+  const float u = a.funi[b];
+  int tok;
+  if (tr.n >= 0) {
+    // Sparse target support, sorted by index into the lower LDS half.
+    const int n = tr.n;
+    load_sorted_by_index(sh, sh.buf, a.sidx_t + trow * kCap, a.sp_t + trow * kCap, n);
+    // residual of entry i (target probability p_i minus q at its index)
+    auto pval = [&](int i) { return __uint_as_float(static_cast<uint32_t>(sh.buf[i])); };
+    auto tidx = [&](int i) { return static_cast<int64_t>(0xffffffffu - static_cast<uint32_t>(sh.buf[i] >> 32)); };
+    bool use_res = false;
+    if (rejected) {
+      float acc = 0.f;
+      for (int i = tid; i < n; i += kT) acc += fmaxf(pval(i) - draft_q<TagD>(a, dr, dsorted, dn, b, len, tidx(i), td), 0.f);
+      const float mass = block_sum(sh, acc);
+      // single-q acceptance falls back to p below 1e-8 (accept_sampling.py:332-340);
+      // dense-q chain sampling always uses the residual (reject_sampling.py:101-121)
+      use_res = a.q_mode == 1 || mass > 1e-8f;
+    }
+    auto val = [&](int i) {
+      const float pi = pval(i);
+      return use_res ? fmaxf(pi - draft_q<TagD>(a, dr, dsorted, dn, b, len, tidx(i), td), 0.f) : pi;
+    };
+    float acc = 0.f;
+    for (int i = tid; i < n; i += kT) acc += val(i);
+    const float total = block_sum(sh, acc);
+    const int hit = total > 0.f ? cdf_find(sh, n, u, val, total) : -1;
+    tok = hit >= 0 ? static_cast<int>(tidx(hit)) : static_cast<int>(a.vocab - 1);
+  } else {
+    // Dense target support: stream the row (and the q source) twice.
+    const XForm f = target_xform(a, b, trow);
+    const float t = a.temps[b];
+    bool use_res = false;
+    if (rejected) {
+      float acc = 0.f;
+      for (int64_t v = tid; v < a.vocab; v += kT)
+        acc += fmaxf(target_p_dense<TagT>(a, tr, b, trow, v, f, t) - draft_q<TagD>(a, dr, dsorted, dn, b, len, v, td), 0.f);
+      use_res = a.q_mode == 1 || block_sum(sh, acc) > 1e-8f;
+    }
+    auto val = [&](int64_t v) {
+      const float pv = target_p_dense<TagT>(a, tr, b, trow, v, f, t);
+      return use_res ? fmaxf(pv - draft_q<TagD>(a, dr, dsorted, dn, b, len, v, td), 0.f) : pv;
+    };
+    float acc = 0.f;
+    for (int64_t v = tid; v < a.vocab; v += kT) acc += val(v);
+    const float total = block_sum(sh, acc);
+    const int hit = total > 0.f ? cdf_find(sh, static_cast<int>(a.vocab), u, [&](int i) { return val(i); }, total) : -1;
+    tok = hit >= 0 ? hit : static_cast<int>(a.vocab - 1);
+  }
+  if (tid == 0) {
+    a.accept[b] = len;
+    a.bonus[b] = tok;
+  }
+  (void)s_tok; (void)s_mass; (void)s_total;
+}
+
+inline uint64_t up256(uint64_t x) { return (x + 255) & ~uint64_t(255); }
+
+int pick_slices(int64_t rows, int64_t vocab, int want_wgs, int max_top_k) {
+  int64_t s = (want_wgs + rows - 1) / rows;
+  int64_t by_len = vocab / 8192;
+  if (by_len < 1) by_len = 1;
+  if (s > by_len) s = by_len;
+  if (s > 16) s = 16;
+  // every slice must be able to hand over top-k plus ties
+  const int64_t need = static_cast<int64_t>(max_top_k) + 64;
+  while (s > 1 && kNBuf / s < need) --s;
+  return static_cast<int>(s < 1 ? 1 : s);
+}
+
+struct Layout {
+  uint64_t counters, scratch;
+  uint64_t off_rec_t, off_sidx_t, off_sp_t, off_rec_d, off_sidx_d, off_sp_d, off_pub_t, off_pubs_t, off_pub_d,
+      off_pubs_d;
+  int s_t, s_d;
+};
+
+Layout layout(int64_t batch, int width, int64_t vocab, int max_top_k) {
+  Layout l{};
+  const int64_t rows = batch * width;
+  l.s_t = pick_slices(rows, vocab, 2048, max_top_k);
+  l.s_d = pick_slices(batch, vocab, 1024, max_top_k);
+  l.counters = up256(4 * rows) + up256(4 * batch);
+  uint64_t o = 0;
+  l.off_rec_t = o; o += up256(sizeof(RowRec) * rows);
+  l.off_sidx_t = o; o += up256(4ull * rows * kCap);
+  l.off_sp_t = o; o += up256(4ull * rows * kCap);
+  l.off_rec_d = o; o += up256(sizeof(RowRec) * batch);
+  l.off_sidx_d = o; o += up256(4ull * batch * kCap);
+  l.off_sp_d = o; o += up256(4ull * batch * kCap);
+  l.off_pub_t = o; o += l.s_t > 1 ? up256(8ull * rows * kNBuf) : 0;
+  l.off_pubs_t = o; o += up256(16ull * rows * l.s_t);
+  l.off_pub_d = o; o += l.s_d > 1 ? up256(8ull * batch * kNBuf) : 0;
+  l.off_pubs_d = o; o += up256(16ull * batch * l.s_d);
+  l.scratch = o;
+  return l;
+}
+
+}  // namespace
+}  // namespace ls
+
+extern "C" int ls_verify_sample_workspace(int64_t batch, int32_t width, int64_t vocab, int32_t max_top_k,
+                                          uint64_t* counter_bytes, uint64_t* scratch_bytes) {
+  LS_CHECK(batch > 0 && width >= 2 && vocab > 0 && counter_bytes && scratch_bytes, LS_ERR_SHAPE,
+           "ls_verify_sample_workspace: bad sizes");
+  const int mk = (max_top_k <= 0 || max_top_k > ls::rs::kCap) ? ls::rs::kCap : max_top_k;
+  const ls::Layout l = ls::layout(batch, width, vocab, mk);
+  *counter_bytes = l.counters;
+  *scratch_bytes = l.scratch;
+  return LS_OK;
+}
+
+extern "C" int ls_verify_sample(const ls_verify_sample_args* in, void* counters, uint64_t counter_bytes, void* scratch,
+                                uint64_t scratch_bytes, void* stream) {
+  using namespace ls;
+  LS_CHECK(in, LS_ERR_VALUE, "ls_verify_sample: null args");
+  const ls_verify_sample_args& x = *in;
+  LS_CHECK(x.batch > 0 && x.width >= 2 && x.width <= 64 && x.vocab > 0 && x.vocab < (int64_t(1) << 31),
+           LS_ERR_SHAPE, "ls_verify_sample: need batch > 0, 2 <= width <= 64, 0 < vocab < 2^31");
+  LS_CHECK(x.logits_row_stride >= x.vocab, LS_ERR_SHAPE, "ls_verify_sample: logits row stride < vocab");
+  LS_CHECK(x.cand_first_col == 0 || x.cand_first_col == 1, LS_ERR_VALUE, "ls_verify_sample: cand_first_col");
+  LS_CHECK(x.logits && x.candidates && x.temperatures && x.uniforms && x.final_uniforms && x.accept_lens && x.bonus,
+           LS_ERR_VALUE, "ls_verify_sample: null required pointer");
+  LS_CHECK(x.q_mode == 0 || x.q_mode == 1, LS_ERR_VALUE, "ls_verify_sample: q_mode must be 0 or 1");
+  LS_CHECK(x.draft, LS_ERR_VALUE, "ls_verify_sample: draft rows required");
+  LS_CHECK(x.q_mode == 1 || x.draft_token_probs, LS_ERR_VALUE, "ls_verify_sample: q_mode 0 needs draft_token_probs");
+  LS_CHECK(x.q_mode == 0 || x.draft_dtype == LS_F32, LS_ERR_DTYPE, "ls_verify_sample: dense q must be fp32");
+  LS_CHECK(!x.pen_bits || (x.pen_rank && x.pen_add), LS_ERR_VALUE, "ls_verify_sample: incomplete penalty tables");
+  LS_CHECK(!x.pen_bits || x.pen_words_stride >= (x.vocab + 31) / 32, LS_ERR_SHAPE,
+           "ls_verify_sample: penalty bitmap stride too small");
+  LS_CHECK(!x.vocab_mask || x.mask_row_stride >= (x.vocab + 31) / 32, LS_ERR_SHAPE,
+           "ls_verify_sample: mask must cover the vocabulary ((V+31)/32 words per row)");
+  const int mk = (x.max_top_k <= 0 || x.max_top_k > rs::kCap) ? rs::kCap : x.max_top_k;
+  const Layout l = layout(x.batch, x.width, x.vocab, mk);
+  LS_CHECK(counters && counter_bytes >= l.counters && scratch && scratch_bytes >= l.scratch, LS_ERR_WORKSPACE,
+           "ls_verify_sample: needs %llu counter and %llu scratch bytes", (unsigned long long)l.counters,
+           (unsigned long long)l.scratch);
+
+  Args a{};
+  a.logits = x.logits; a.lrs = x.logits_row_stride;
+  a.cand = x.candidates; a.csb = x.cand_stride_b; a.csk = x.cand_stride_k; a.cfirst = x.cand_first_col;
+  a.batch = x.batch; a.width = x.width; a.vocab = x.vocab;
+  a.temps = x.temperatures; a.top_ks = x.top_ks; a.top_ps = x.top_ps; a.min_ps = x.min_ps;
+  a.pbits = x.pen_bits; a.prank = x.pen_rank; a.pws = x.pen_words_stride; a.padd = x.pen_add;
+  a.pas = x.pen_add_stride; a.prep = x.pen_repetition; a.quirk = x.pen_verify_quirk;
+  a.mask = reinterpret_cast<const uint32_t*>(x.vocab_mask); a.mrs = x.mask_row_stride;
+  a.mask_per_request = x.mask_per_request;
+  a.q_mode = x.q_mode; a.dtp = x.draft_token_probs; a.dtp_sb = x.dtp_stride_b;
+  a.draft = x.draft; a.dsb = x.draft_stride_b; a.dsk = x.draft_stride_k;
+  a.d_temps = x.draft_temperatures; a.d_top_ks = x.draft_top_ks; a.d_top_ps = x.draft_top_ps;
+  a.d_min_ps = x.draft_min_ps;
+  a.uni = x.uniforms; a.usb = x.uniform_stride_b; a.funi = x.final_uniforms;
+  a.accept = x.accept_lens; a.bonus = x.bonus; a.p_cand_out = x.p_cand_out; a.status = x.status;
+  char* c = static_cast<char*>(counters);
+  const int64_t rows = x.batch * x.width;
+  a.cnt_t = reinterpret_cast<uint32_t*>(c);
+  a.cnt_d = reinterpret_cast<uint32_t*>(c + up256(4 * rows));
+  char* s = static_cast<char*>(scratch);
+  a.rec_t = reinterpret_cast<RowRec*>(s + l.off_rec_t);
+  a.sidx_t = reinterpret_cast<int32_t*>(s + l.off_sidx_t);
+  a.sp_t = reinterpret_cast<float*>(s + l.off_sp_t);
+  a.rec_d = reinterpret_cast<RowRec*>(s + l.off_rec_d);
+  a.sidx_d = reinterpret_cast<int32_t*>(s + l.off_sidx_d);
+  a.sp_d = reinterpret_cast<float*>(s + l.off_sp_d);
+  a.pub_t = reinterpret_cast<uint64_t*>(s + l.off_pub_t);
+  a.pubs_t = reinterpret_cast<uint64_t*>(s + l.off_pubs_t);
+  a.pub_d = reinterpret_cast<uint64_t*>(s + l.off_pub_d);
+  a.pubs_d = reinterpret_cast<uint64_t*>(s + l.off_pubs_d);
+  a.s_t = l.s_t;
+  a.s_d = l.s_d;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+
+  const dim3 g_t(static_cast<unsigned>(rows * l.s_t)), g_d(static_cast<unsigned>(x.batch * l.s_d)),
+      g_r(static_cast<unsigned>(x.batch));
+  const bool tvec_ok = aligned16(x.logits);
+  const bool dvec_ok = aligned16(x.draft);
+#define LS_RUN(TT, TD, CT)                                                                                    \
+  do {                                                                                                        \
+    using TS = typename TT::storage;                                                                          \
+    using DS = typename TD::storage;                                                                          \
+    const bool tv = tvec_ok && (x.logits_row_stride * sizeof(TS)) % 16 == 0;                                  \
+    const bool dv = dvec_ok && (x.draft_stride_b * sizeof(DS)) % 16 == 0 && (x.draft_stride_k * sizeof(DS)) % 16 == 0; \
+    if (tv) target_scan_kernel<TT, true, CT><<<g_t, rs::kT, 0, st>>>(a);                                     \
+    else target_scan_kernel<TT, false, CT><<<g_t, rs::kT, 0, st>>>(a);                                       \
+    LS_LAUNCH_CHECK();                                                                                        \
+    if (x.q_mode == 0) {                                                                                      \
+      if (dv) draft_scan_kernel<TD, true, CT><<<g_d, rs::kT, 0, st>>>(a);                                    \
+      else draft_scan_kernel<TD, false, CT><<<g_d, rs::kT, 0, st>>>(a);                                      \
+      LS_LAUNCH_CHECK();                                                                                      \
+    }                                                                                                         \
+    resolve_kernel<TT, TD, CT><<<g_r, rs::kT, 0, st>>>(a);                                                    \
+    LS_LAUNCH_CHECK();                                                                                        \
+    return LS_OK;                                                                                             \
+  } while (0)
+#define LS_CAND(TT, TD)                                             \
+  if (x.candidates_dtype == LS_I32) LS_RUN(TT, TD, int32_t);        \
+  else if (x.candidates_dtype == LS_I64) LS_RUN(TT, TD, int64_t);   \
+  else return fail(LS_ERR_DTYPE, "ls_verify_sample: candidates must be int32 or int64");
+#define LS_DRAFT(TT)                                                 \
+  if (x.draft_dtype == LS_F32) { LS_CAND(TT, F32) }                  \
+  else if (x.draft_dtype == LS_BF16) { LS_CAND(TT, BF16) }           \
+  else return fail(LS_ERR_DTYPE, "ls_verify_sample: draft rows must be fp32 or bf16");
+  if (x.logits_dtype == LS_BF16) { LS_DRAFT(BF16) }
+  if (x.logits_dtype == LS_F32) { LS_DRAFT(F32) }
+  if (x.logits_dtype == LS_F16) { LS_DRAFT(F16) }
+#undef LS_DRAFT
+#undef LS_CAND
+#undef LS_RUN
+  return fail(LS_ERR_DTYPE, "ls_verify_sample: logits must be bf16, fp16 or fp32");
+}

@@ -1,0 +1,114 @@
+"""Penalties and vocabulary bitmask on the GPU (drop-ins for the reference's
+logit-adjustment call sites).
+
+``SRT`` = ``vendor/sglang/python/sglang/srt``.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+
+from . import _lib
+
+
+@dataclass
+class PenaltyTables:
+    """Compact per-request penalty state (see ``ls_penalty_tables`` in
+    include/longspark_amd.h): presence bitmap, popcount ranks, additive value
+    per present token, repetition scale, and the penalty application mode."""
+    bits: torch.Tensor          # [B, ceil(V/32)] int32 (bit pattern)
+    rank: torch.Tensor          # [B, ceil(V/32)] int32
+    add: torch.Tensor           # [B, H] float32
+    distinct: torch.Tensor      # [B] int32
+    repetition: Optional[torch.Tensor]  # [B] float32 or None
+    verify_quirk: bool = False
+
+
+def build_penalty_tables(history: torch.Tensor, vocab: int, *, frequency=None, presence=None, repetition=None,
+                         history_lens: Optional[torch.Tensor] = None, verify_quirk: bool = False) -> PenaltyTables:
+    """Penalty tables from each request's output-token history ``[B, H]`` int32.
+
+    ``frequency`` / ``presence`` / ``repetition`` are per-request ``[B]``
+    values (None = the penaliser is off), as the reference penalisers take
+    them from each request's sampling params
+    (SRT/sampling/penaltylib/{frequency,presence,repetition}_penalty.py).
+    ``verify_quirk`` selects the verify-path application of
+    SRT/speculative/dflash_utils.py:176-191 (bias built on zeros).
+    """
+    what = "build_penalty_tables"
+    dev = _lib.require_cuda(history, frequency, presence, repetition, history_lens, what=what)
+    if history.ndim != 2 or history.dtype != torch.int32 or history.stride(1) != 1:
+        raise ValueError(f"{what}: history must be [B, H] int32 with unit column stride")
+    batch, cap = history.shape
+    words = (vocab + 31) // 32
+    bits = torch.empty(batch, words, dtype=torch.int32, device=dev)
+    rank = torch.empty(batch, words, dtype=torch.int32, device=dev)
+    add = torch.empty(batch, max(cap, 1), dtype=torch.float32, device=dev)
+    distinct = torch.empty(batch, dtype=torch.int32, device=dev)
+
+    def vec(t, name):
+        if t is None:
+            return None
+        t = torch.as_tensor(t, device=dev, dtype=torch.float32).reshape(-1)
+        if t.numel() == 1 and batch > 1:
+            t = t.expand(batch).contiguous()
+        if t.shape != (batch,):
+            raise ValueError(f"{what}: {name} must have one value per request")
+        return t.contiguous()
+
+    frequency, presence, repetition = vec(frequency, "frequency"), vec(presence, "presence"), vec(repetition, "repetition")
+    if history_lens is not None:
+        history_lens = history_lens.to(torch.int32).contiguous()
+    _lib.call("ls_penalty_tables", history.data_ptr(), history.stride(0), _lib.ptr(history_lens), batch, cap, vocab,
+              _lib.ptr(frequency), _lib.ptr(presence), bits.data_ptr(), rank.data_ptr(), words, add.data_ptr(),
+              add.shape[1], distinct.data_ptr(), _lib.stream_of(dev))
+    return PenaltyTables(bits=bits, rank=rank, add=add, distinct=distinct, repetition=repetition,
+                         verify_quirk=verify_quirk)
+
+
+def adjust_logits_(logits: torch.Tensor, *, rows_per_request: int, tables: Optional[PenaltyTables] = None,
+                   vocab_mask: Optional[torch.Tensor] = None, mask_per_request: bool = False) -> None:
+    """In place on ``[B*rows_per_request, V]`` logits: penalties, then the bitmask.
+
+    Drop-in body of SRT/speculative/dflash_utils.py:127-213
+    (``apply_dflash_verify_logits_adjustments``) with the penalty state given
+    as tables.
+    """
+    what = "adjust_logits_"
+    dev = _lib.require_cuda(logits, vocab_mask, what=what)
+    if logits.ndim != 2 or logits.stride(1) != 1:
+        raise ValueError(f"{what}: logits must be [rows, V] with unit column stride")
+    rows, vocab = logits.shape
+    if vocab_mask is not None:
+        if vocab_mask.dtype != torch.int32 or vocab_mask.ndim != 2 or vocab_mask.stride(1) != 1:
+            raise ValueError(f"{what}: vocab_mask must be [rows or B, W] int32")
+        expect = rows // rows_per_request if mask_per_request else rows
+        if vocab_mask.shape[0] != expect:
+            raise ValueError(f"{what}: vocab_mask has {vocab_mask.shape[0]} rows, expected {expect}")
+    t = tables
+    _lib.call("ls_adjust_logits", logits.data_ptr(), _lib.dtype_code(logits), logits.stride(0), rows, vocab,
+              rows_per_request,
+              _lib.ptr(t.bits) if t else None, _lib.ptr(t.rank) if t else None, t.bits.stride(0) if t else 0,
+              _lib.ptr(t.add) if t else None, t.add.stride(0) if t else 0,
+              _lib.ptr(t.repetition) if t else None, int(bool(t and t.verify_quirk)),
+              _lib.ptr(vocab_mask), vocab_mask.stride(0) if vocab_mask is not None else 0,
+              rows_per_request if mask_per_request else 1,
+              vocab_mask.shape[1] if vocab_mask is not None else 0, _lib.stream_of(dev))
+
+
+def apply_token_bitmask_inplace(logits: torch.Tensor, bitmask: torch.Tensor) -> None:
+    """SRT/constrained/triton_ops/bitmask_ops.py:84-141 (without ``indices``):
+    bit 0 of ``bitmask[row, v >> 5] >> (v & 31)`` sets ``-inf``; only the first
+    ``min(V, 32 * W)`` columns are touched."""
+    if logits.ndim == 1:
+        logits = logits.unsqueeze(0)
+    if bitmask.ndim == 1:
+        bitmask = bitmask.unsqueeze(0)
+    if bitmask.shape[1] > (logits.shape[1] + 31) // 32:
+        raise ValueError("bitmask width too large for the logits width")
+    if bitmask.shape[0] != logits.shape[0]:
+        raise ValueError("batch size mismatch between logits and bitmask")
+    adjust_logits_(logits, rows_per_request=1, vocab_mask=bitmask)

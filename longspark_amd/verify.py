@@ -118,3 +118,136 @@ def compute_greedy_accept_len_and_bonus_from_logits(*, candidates, target_logits
     accept, bonus, _ = verify_greedy(logits=target_logits, candidates=candidates, width=draft_token_num,
                                      cand_first_col=1)
     return accept, bonus
+
+
+# --------------------------------------------------------------------------
+# stochastic verification
+# --------------------------------------------------------------------------
+
+def _per_request(t, batch, dtype, dev, name, what):
+    if t is None:
+        return None
+    t = torch.as_tensor(t, device=dev).reshape(-1)
+    if t.numel() == 1 and batch > 1:
+        t = t.expand(batch)
+    if t.shape != (batch,):
+        raise ValueError(f"{what}: {name} must have one value per request")
+    return t.to(dtype).contiguous()
+
+
+def verify_sample(*, logits: torch.Tensor, candidates: torch.Tensor, width: int, temperatures,
+                  uniforms: torch.Tensor, final_uniforms: torch.Tensor, top_ks=None, top_ps=None, min_ps=None,
+                  max_top_k: Optional[int] = None, draft_token_probs: Optional[torch.Tensor] = None,
+                  draft_logits: Optional[torch.Tensor] = None, draft_probs: Optional[torch.Tensor] = None,
+                  draft_temperatures=None, draft_top_ks=None, draft_top_ps=None, draft_min_ps=None,
+                  penalties=None, vocab_mask: Optional[torch.Tensor] = None, mask_per_request: bool = False,
+                  cand_first_col: int = 1, return_p_cand: bool = False, check: bool = False):
+    """Fused stochastic verify of a drafted block (one call, three kernels).
+
+    Target: ``logits`` ``[B*width, V]`` (bf16/fp16/fp32) with penalties
+    (``penalties``: :class:`longspark_amd.penalties.PenaltyTables`) and a packed
+    ``vocab_mask`` applied on the fly, then temperature / top-k / top-p /
+    min-p (per-request ``[B]`` values; None disables).
+    Draft: either ``draft_token_probs [B, width-1]`` (q of each drafted token)
+    with ``draft_logits [B, width-1, V]`` (q row rebuilt at the rejection with
+    the ``draft_*`` parameters; pure temperature when they are None), or dense
+    ``draft_probs [B, width-1, V]`` fp32 (q read directly).
+    Randomness: ``uniforms [B, width-1]`` and ``final_uniforms [B]`` fp32.
+    Returns ``(accept_lens i32[B], bonus i64[B])`` (plus the per-drafted-token
+    target probabilities ``[B, width-1]`` with ``return_p_cand``).  With
+    ``check`` the call synchronises and raises if a request exceeded the
+    kernel's support capacity (such requests get -1 in both outputs).
+    """
+    what = "verify_sample"
+    logits = _rows_view(logits, width, what)
+    draft = draft_probs if draft_probs is not None else draft_logits
+    dev = _lib.require_cuda(logits, candidates, uniforms, final_uniforms, draft, draft_token_probs, vocab_mask,
+                            what=what)
+    if candidates.ndim != 2 or candidates.dtype not in (torch.int32, torch.int64):
+        raise ValueError(f"{what}: candidates must be [B, C] int32/int64")
+    batch = candidates.shape[0]
+    vocab = logits.shape[1]
+    g = width - 1
+    if width < 2 or logits.shape[0] != batch * width:
+        raise ValueError(f"{what}: expected {batch}*{width} logits rows, got {logits.shape[0]}")
+    if candidates.shape[1] < cand_first_col + g:
+        raise ValueError(f"{what}: candidates need {cand_first_col + g} columns")
+    if draft is None:
+        raise ValueError(f"{what}: draft_logits (with draft_token_probs) or draft_probs is required")
+    q_mode = 1 if draft_probs is not None else 0
+    if draft.ndim != 3 or draft.shape != (batch, g, vocab) or draft.stride(2) != 1:
+        raise ValueError(f"{what}: draft rows must be [B, width-1, V] with unit vocabulary stride")
+    if q_mode == 1 and draft.dtype != torch.float32:
+        raise ValueError(f"{what}: draft_probs must be fp32")
+    if q_mode == 0:
+        if draft_token_probs is None or draft_token_probs.shape != (batch, g) or \
+                draft_token_probs.dtype != torch.float32:
+            raise ValueError(f"{what}: draft_token_probs must be [B, width-1] fp32")
+        draft_token_probs = draft_token_probs.contiguous()
+    if uniforms.shape != (batch, g) or uniforms.dtype != torch.float32 or uniforms.stride(1) != 1:
+        raise ValueError(f"{what}: uniforms must be [B, width-1] fp32")
+    if final_uniforms.shape != (batch,) or final_uniforms.dtype != torch.float32:
+        raise ValueError(f"{what}: final_uniforms must be [B] fp32")
+    final_uniforms = final_uniforms.contiguous()
+    temps = _per_request(temperatures, batch, torch.float32, dev, "temperatures", what)
+    if temps is None:
+        raise ValueError(f"{what}: temperatures are required")
+    top_ks = _per_request(top_ks, batch, torch.int32, dev, "top_ks", what)
+    top_ps = _per_request(top_ps, batch, torch.float32, dev, "top_ps", what)
+    min_ps = _per_request(min_ps, batch, torch.float32, dev, "min_ps", what)
+    d_t = _per_request(draft_temperatures, batch, torch.float32, dev, "draft_temperatures", what)
+    d_k = _per_request(draft_top_ks, batch, torch.int32, dev, "draft_top_ks", what)
+    d_p = _per_request(draft_top_ps, batch, torch.float32, dev, "draft_top_ps", what)
+    d_m = _per_request(draft_min_ps, batch, torch.float32, dev, "draft_min_ps", what)
+    if vocab_mask is not None:
+        words = (vocab + 31) // 32
+        rows_m = batch if mask_per_request else batch * width
+        if vocab_mask.dtype != torch.int32 or vocab_mask.shape != (rows_m, words) or vocab_mask.stride(1) != 1:
+            raise ValueError(f"{what}: vocab_mask must be [{rows_m}, {words}] int32")
+    mk = 0 if max_top_k is None else int(max_top_k)
+
+    accept = torch.empty(batch, dtype=torch.int32, device=dev)
+    bonus = torch.empty(batch, dtype=torch.int64, device=dev)
+    p_cand = torch.empty(batch, g, dtype=torch.float32, device=dev) if return_p_cand else None
+    status = torch.zeros(1, dtype=torch.int32, device=dev)
+    a = _lib.VerifySampleArgs()
+    a.logits, a.logits_dtype, a.logits_row_stride = logits.data_ptr(), _lib.dtype_code(logits), logits.stride(0)
+    a.candidates, a.candidates_dtype = candidates.data_ptr(), _lib.dtype_code(candidates)
+    a.cand_stride_b, a.cand_stride_k, a.cand_first_col = candidates.stride(0), candidates.stride(1), cand_first_col
+    a.batch, a.width, a.vocab = batch, width, vocab
+    a.temperatures, a.top_ks, a.top_ps, a.min_ps = _lib.ptr(temps), _lib.ptr(top_ks), _lib.ptr(top_ps), _lib.ptr(min_ps)
+    a.max_top_k = mk
+    t = penalties
+    if t is not None:
+        a.pen_bits, a.pen_rank, a.pen_words_stride = t.bits.data_ptr(), t.rank.data_ptr(), t.bits.stride(0)
+        a.pen_add, a.pen_add_stride = t.add.data_ptr(), t.add.stride(0)
+        a.pen_repetition, a.pen_verify_quirk = _lib.ptr(t.repetition), int(bool(t.verify_quirk))
+    if vocab_mask is not None:
+        a.vocab_mask, a.mask_row_stride, a.mask_per_request = vocab_mask.data_ptr(), vocab_mask.stride(0), \
+            int(mask_per_request)
+    a.q_mode = q_mode
+    if q_mode == 0:
+        a.draft_token_probs, a.dtp_stride_b = draft_token_probs.data_ptr(), draft_token_probs.stride(0)
+    a.draft, a.draft_dtype, a.draft_stride_b, a.draft_stride_k = draft.data_ptr(), _lib.dtype_code(draft), \
+        draft.stride(0), draft.stride(1)
+    a.draft_temperatures, a.draft_top_ks = _lib.ptr(d_t), _lib.ptr(d_k)
+    a.draft_top_ps, a.draft_min_ps = _lib.ptr(d_p), _lib.ptr(d_m)
+    a.uniforms, a.uniform_stride_b, a.final_uniforms = uniforms.data_ptr(), uniforms.stride(0), \
+        final_uniforms.data_ptr()
+    a.accept_lens, a.bonus, a.p_cand_out, a.status = accept.data_ptr(), bonus.data_ptr(), _lib.ptr(p_cand), \
+        status.data_ptr()
+    cnt, scr = _lib.workspaces.get(*_lib.workspace_sizes("ls_verify_sample_workspace", batch, width, vocab, mk), dev)
+    _lib.call("ls_verify_sample", ctypes_byref(a), cnt.data_ptr(), cnt.numel(), scr.data_ptr(), scr.numel(),
+              _lib.stream_of(dev))
+    if check:
+        torch.cuda.synchronize(dev)
+        if int(status.item()) != 0:
+            raise RuntimeError(f"{what}: a request's sampling support exceeded the kernel capacity")
+    if return_p_cand:
+        return accept, bonus, p_cand
+    return accept, bonus
+
+
+def ctypes_byref(struct):
+    import ctypes
+    return ctypes.byref(struct)

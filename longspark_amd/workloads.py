@@ -100,3 +100,69 @@ class SamplingParams:
     def to(self, device):
         return SamplingParams(*(t.to(device) for t in (self.temperatures, self.top_ks, self.top_ps,
                                                         self.min_ps)))
+
+
+def sampling_distribution(logits: torch.Tensor, temperature: float, top_k: int, top_p: float,
+                          min_p: float) -> torch.Tensor:
+    """Dense ``[rows, V]`` fp32 distribution after temperature / top-k / top-p /
+    min-p, built with plain torch ops (used to draw synthetic drafted tokens)."""
+    rows, vocab = logits.shape
+    scaled = logits.float() / temperature
+    if top_k < vocab:
+        vals, idx = torch.topk(scaled, top_k, dim=-1)
+    else:
+        vals, idx = torch.sort(scaled, dim=-1, descending=True)
+    p = torch.softmax(vals, dim=-1)
+    if top_p < 1.0:
+        cum = p.cumsum(-1)
+        p = torch.where(cum - p > top_p, torch.zeros_like(p), p)
+        p = p / p.sum(-1, keepdim=True)
+    if min_p > 0.0:
+        p = torch.where(p < p[:, :1] * min_p, torch.zeros_like(p), p)
+        p = p / p.sum(-1, keepdim=True)
+    return torch.zeros(rows, vocab, device=logits.device).scatter_(1, idx, p)
+
+
+def stochastic_inputs(batch: int, width: int = 16, vocab: int = VOCAB, *, seed: int = 0, temperature: float = 0.7,
+                      top_k: int = VOCAB, top_p: float = 1.0, min_p: float = 0.0, history_len: int = 0,
+                      repetition: float = 1.0, presence: float = 0.0, frequency: float = 0.0,
+                      mask_density: Optional[float] = None, dtype=torch.bfloat16, device="cpu", gen_device="cpu"):
+    """Inputs of one stochastic verify round.
+
+    Target logits as in :func:`greedy_inputs`; draft logits = target + N(0, 1)
+    in fp32; q = the draft distribution under the same temperature / top-k /
+    top-p / min-p; drafted tokens are drawn from q; uniforms U(0, 1).
+    Optional: a Zipf(1.1) history of ``history_len`` tokens per request with
+    repetition / presence / frequency values, and a per-row packed bitmask
+    with about ``mask_density`` of the bits set (the drafted token's bit set
+    with probability 0.8).  Returns a dict of tensors on ``device``.
+    """
+    logits, cand = greedy_inputs(batch, width, vocab, seed=seed, dtype=dtype, device=gen_device,
+                                 gen_device=gen_device)
+    g = width - 1
+    gen = _gen(seed + 1, gen_device)
+    target = logits.float().view(batch, width, vocab)
+    draft = target[:, :g] + torch.randn(batch, g, vocab, generator=gen, device=gen_device)
+    q = sampling_distribution(draft.reshape(-1, vocab), temperature, top_k, top_p, min_p)
+    drafted = torch.multinomial(q, 1, generator=gen).view(batch, g)
+    cand = cand.to(torch.int64)
+    cand[:, 1:] = drafted
+    dtp = q.view(batch, g, vocab).gather(2, drafted[..., None]).squeeze(-1).contiguous()
+    uniforms = torch.rand(batch, g, generator=gen, device=gen_device)
+    final = torch.rand(batch, generator=gen, device=gen_device)
+    out = dict(logits=logits, candidates=cand.to(torch.int32), draft_logits=draft.contiguous(),
+               draft_token_probs=dtp, uniforms=uniforms, final_uniforms=final,
+               params=SamplingParams.uniform(batch, temperature=temperature, top_k=top_k, top_p=top_p,
+                                             min_p=min_p, device=gen_device))
+    if history_len > 0:
+        out["history"] = zipf_history(batch, history_len, vocab, seed=seed + 2, device=gen_device)
+        out["repetition"] = torch.full((batch,), repetition, device=gen_device)
+        out["presence"] = torch.full((batch,), presence, device=gen_device)
+        out["frequency"] = torch.full((batch,), frequency, device=gen_device)
+    if mask_density is not None:
+        force = torch.cat([cand[:, 1:], cand[:, :1]], dim=1).reshape(-1)  # row j verifies cand[j+1]
+        out["vocab_mask"] = random_bitmask(batch * width, vocab, density=mask_density, seed=seed + 3,
+                                           force_tokens=force, device=gen_device)
+    for k, v in list(out.items()):
+        out[k] = v.to(device) if isinstance(v, (torch.Tensor, SamplingParams)) else v
+    return out

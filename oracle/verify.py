@@ -219,9 +219,14 @@ def apply_verify_adjustments(logits, *, additive=None, scaling=None, bitmask=Non
             pen.add_(additive)
         if scaling is not None:
             apply_scaling_penalties(pen, scaling)
-        if bitmask is not None:
+        per_request_mask = bitmask is not None and bitmask.shape[0] == bs and rows_per_request > 1
+        if per_request_mask:
             apply_token_bitmask(pen, bitmask)
         view.add_(pen[:, None, :])
+        if bitmask is not None and not per_request_mask:
+            # The reference's verify path carries one mask row per request; a
+            # per-row mask sets -inf row by row, which adding -inf would do.
+            apply_token_bitmask(logits, bitmask)
         return
     if additive is not None:
         view.add_(additive[:, None, :])

@@ -1,0 +1,121 @@
+"""Fused stochastic verify on the GPU vs the CPU oracle.
+
+Workloads (full 151,936 vocabulary unless stated):
+  * temperature 0.7, top-k 50, top-p 0.95, batch 8, block 16;
+  * penalised and masked: repetition 1.1 / presence 0.5 / frequency 0.2 over a
+    4096-token Zipf(1.1) history, per-row bitmask with ~30% of bits set,
+    temperature 0.8, top-p 0.9, min-p 0.05 (batch 4; the workload's batch 32
+    runs in the benchmark);
+  * top-k 50 / top-p 0.95 with repetition 1.05 over a 2048-token history
+    (batch 16; batch 128 runs in the benchmark);
+  * pure temperature (dense support), batch 4;
+  * dense draft probabilities (q_mode 1), batch 4;
+  * the verify-path penalty quirk;
+  * small vocabularies with heavy ties and top-k 1 / 5 / 50 / >= V.
+Bit-exact accept lengths and tokens except near-ties (tests/verify_ref.py);
+drafted-token target probabilities within 1e-5 relative.
+"""
+
+import pytest
+import torch
+
+from longspark_amd import penalties, verify, workloads
+from tests import verify_ref as vr
+
+pytestmark = pytest.mark.gpu
+
+
+def run_kernel(dev, d, *, verify_quirk=False, draft_params=True, dense_q=None):
+    p = d["params"]
+    tables = None
+    if "history" in d:
+        tables = penalties.build_penalty_tables(d["history"].to(dev), d["logits"].shape[1],
+                                                frequency=d["frequency"].to(dev), presence=d["presence"].to(dev),
+                                                repetition=d["repetition"].to(dev), verify_quirk=verify_quirk)
+    kw = {}
+    if draft_params:
+        kw = dict(draft_top_ks=p.top_ks.to(dev), draft_top_ps=p.top_ps.to(dev), draft_min_ps=p.min_ps.to(dev))
+    width = d["candidates"].shape[1]
+    if dense_q is not None:
+        kw = dict(draft_probs=dense_q.to(dev))
+    else:
+        kw.update(draft_logits=d["draft_logits"].to(dev), draft_token_probs=d["draft_token_probs"].to(dev))
+    acc, bonus, pc = verify.verify_sample(
+        logits=d["logits"].to(dev), candidates=d["candidates"].to(dev), width=width,
+        temperatures=p.temperatures.to(dev), top_ks=p.top_ks.to(dev), top_ps=p.top_ps.to(dev),
+        min_ps=p.min_ps.to(dev), uniforms=d["uniforms"].to(dev), final_uniforms=d["final_uniforms"].to(dev),
+        penalties=tables, vocab_mask=d["vocab_mask"].to(dev) if "vocab_mask" in d else None,
+        return_p_cand=True, check=True, **kw)
+    torch.cuda.synchronize()
+    return acc.cpu(), bonus.cpu(), pc.cpu()
+
+
+def check_case(dev, d, *, verify_quirk=False, label=""):
+    print(f"verify_sample case {label}: B={d['candidates'].shape[0]} V={d['logits'].shape[1]}", flush=True)
+    acc, bonus, pc = run_kernel(dev, d, verify_quirk=verify_quirk)
+    c = vr.oracle_inputs(d, verify_quirk=verify_quirk)
+    lens_r, bonus_r, probs_r = vr.run_oracle(c)
+    bad, exempt, msgs = vr.classify(c, acc, bonus, lens_r, bonus_r, probs_r, pc)
+    for m in msgs:
+        print(m)
+    assert not bad, f"{len(bad)} requests differ beyond the tie contract: {msgs}"
+    assert len(exempt) <= max(1, acc.numel() // 8), f"too many tie exemptions: {msgs}"
+    return acc, bonus
+
+
+def test_topk_topp_full_vocab(dev):
+    d = workloads.stochastic_inputs(8, 16, seed=11, temperature=0.7, top_k=50, top_p=0.95)
+    acc, _ = check_case(dev, d, label="T0.7 k50 p0.95")
+    assert int(acc.min()) >= 0
+
+
+def test_penalties_mask_topp_minp(dev):
+    d = workloads.stochastic_inputs(4, 16, seed=12, temperature=0.8, top_p=0.9, min_p=0.05, history_len=4096,
+                                    repetition=1.1, presence=0.5, frequency=0.2, mask_density=0.3)
+    check_case(dev, d, label="penalties+mask T0.8 p0.9 minp0.05")
+
+
+def test_topk_repetition_history(dev):
+    d = workloads.stochastic_inputs(16, 16, seed=13, temperature=0.7, top_k=50, top_p=0.95, history_len=2048,
+                                    repetition=1.05)
+    check_case(dev, d, label="k50 p0.95 rep1.05")
+
+
+def test_verify_quirk(dev):
+    d = workloads.stochastic_inputs(4, 16, seed=14, temperature=0.8, top_k=40, top_p=0.9, history_len=1024,
+                                    repetition=1.2, presence=0.4, frequency=0.3, mask_density=0.5)
+    check_case(dev, d, verify_quirk=True, label="verify quirk")
+
+
+def test_pure_temperature_dense(dev):
+    d = workloads.stochastic_inputs(4, 8, 20000, seed=15, temperature=1.3)
+    check_case(dev, d, label="pure temperature")
+
+
+@pytest.mark.parametrize("top_k", [1, 5, 50, 1000, 2000])
+def test_small_vocab_ties(dev, top_k):
+    # integer-valued logits -> many exact ties at every threshold
+    d = workloads.stochastic_inputs(6, 8, 2000, seed=16 + top_k, temperature=1.0, top_k=top_k, top_p=0.8)
+    g = torch.Generator().manual_seed(top_k)
+    d["logits"] = torch.randint(-4, 5, d["logits"].shape, generator=g).to(torch.bfloat16)
+    check_case(dev, d, label=f"ties k={top_k}")
+
+
+def test_dense_draft_probs(dev):
+    d = workloads.stochastic_inputs(4, 8, 30000, seed=17, temperature=0.9, top_k=30, top_p=0.9)
+    from oracle import verify as ov
+    p = d["params"]
+    q = ov.target_probs(d["draft_logits"].reshape(-1, 30000), temperatures=p.temperatures, top_ks=p.top_ks,
+                        top_ps=p.top_ps, min_ps=p.min_ps, rows_per_request=7).view(4, 7, 30000)
+    acc, bonus, _ = run_kernel(dev, d, dense_q=q)
+    c = vr.oracle_inputs(d)
+    x = c["logits"].float()
+    probs = ov.target_probs(x, temperatures=p.temperatures, top_ks=p.top_ks, top_ps=p.top_ps, min_ps=p.min_ps,
+                            rows_per_request=8).view(4, 8, 30000)
+    _, _, _ = None, None, None
+    preds, aidx, anum = ov.chain_speculative_sampling(
+        candidates=c["candidates"].long(), uniform_samples=c["uniforms"], uniform_final=c["final_uniforms"],
+        target_probs_3d=probs, draft_probs_3d=q)
+    ref_bonus = preds[aidx[torch.arange(4), anum.long()].long()]
+    assert torch.equal(acc, anum), (acc, anum)
+    assert torch.equal(bonus, ref_bonus.long()), (bonus, ref_bonus)
