@@ -102,8 +102,111 @@ class GreedyVerify:
                 f"fp32 logits, median of {n} runs", "threads": threads}
 
 
-WORKLOADS = {w.name: w for w in (GreedyVerify,)}
-DEFAULT_WORKLOAD = "verify_greedy"
+class HipEvents:
+    """hipEvent_t handles from the HIP runtime (for timing kernels that one C ABI
+    call launches back to back on a stream)."""
+
+    def __init__(self, n):
+        import ctypes
+        self.ct = ctypes
+        self.hip = ctypes.CDLL("libamdhip64.so")
+        self.hip.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint]
+        self.hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+        self.hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        self.handles = (ctypes.c_void_p * n)()
+        for i in range(n):
+            h = ctypes.c_void_p()
+            if self.hip.hipEventCreateWithFlags(ctypes.byref(h), 0) != 0:
+                raise RuntimeError("hipEventCreateWithFlags failed")
+            self.handles[i] = h
+
+    def group(self, i, k):
+        """ctypes array view of events [i*k, (i+1)*k)."""
+        return (self.ct.c_void_p * k).from_address(self.ct.addressof(self.handles) + i * k * self.ct.sizeof(self.ct.c_void_p))
+
+    def elapsed_ms(self, a, b):
+        ms = self.ct.c_float()
+        if self.hip.hipEventElapsedTime(self.ct.byref(ms), self.handles[a], self.handles[b]) != 0:
+            raise RuntimeError("hipEventElapsedTime failed")
+        return ms.value
+
+
+class StochasticVerify:
+    """Fused stochastic verify, batch 128 x block 16 x vocab 151,936 bf16:
+    temperature 0.7, top-k 50, top-p 0.95, repetition 1.05 over a 2048-token
+    Zipf(1.1) history; draft rows fp32; one penalty-table build + one fused
+    verify per step."""
+
+    name = "verify_sample"
+
+    def __init__(self, dev, batch=128, width=16, vocab=V):
+        from longspark_amd import workloads
+        self.dev, self.batch, self.width, self.vocab = dev, batch, width, vocab
+        self.cfg = dict(temperature=0.7, top_k=50, top_p=0.95, history_len=2048, repetition=1.05)
+        self.d = workloads.stochastic_inputs(batch, width, vocab, seed=2025, device=dev, gen_device=dev, **self.cfg)
+        self.rows = batch * width
+        self.kernel = "target_scan_kernel"
+        self.kernel_bytes = self.rows * vocab * 2          # every target logit once
+        # whole verify, as counted for the workload: logits + one fp32 draft row per
+        # request + the int32 history
+        self.bytes = self.kernel_bytes + batch * vocab * 4 + batch * self.cfg["history_len"] * 4
+        self.events = None
+        self.step_idx = 0
+
+    def arm_timing(self, steps):
+        self.events = HipEvents(4 * steps)
+        self.step_idx = 0
+
+    def step(self):
+        from longspark_amd import penalties, verify
+        d, p = self.d, self.d["params"]
+        tables = penalties.build_penalty_tables(d["history"], self.vocab, repetition=d["repetition"])
+        ev = None
+        if self.events is not None:
+            ev = self.events.group(self.step_idx, 4)
+            self.step_idx += 1
+        return verify.verify_sample(
+            logits=d["logits"], candidates=d["candidates"], width=self.width, temperatures=p.temperatures,
+            top_ks=p.top_ks, top_ps=p.top_ps, min_ps=p.min_ps, max_top_k=50, draft_logits=d["draft_logits"],
+            draft_token_probs=d["draft_token_probs"], draft_top_ks=p.top_ks, draft_top_ps=p.top_ps,
+            uniforms=d["uniforms"], final_uniforms=d["final_uniforms"], penalties=tables, timing_events=ev)
+
+    def kernel_times_ms(self):
+        n = self.step_idx
+        e = self.events
+        scan = sum(e.elapsed_ms(4 * i, 4 * i + 1) for i in range(n)) / n
+        draft = sum(e.elapsed_ms(4 * i + 1, 4 * i + 2) for i in range(n)) / n
+        resolve = sum(e.elapsed_ms(4 * i + 2, 4 * i + 3) for i in range(n)) / n
+        return {"target_scan_kernel": scan, "fallback+draft_scan_kernels": draft, "resolve_kernel": resolve}
+
+    def config(self):
+        return {"workload": f"fused stochastic verify B={self.batch} K={self.width} V={self.vocab} bf16, T 0.7, "
+                            "top-k 50, top-p 0.95, repetition 1.05 over a 2048-token Zipf history; draft rows fp32",
+                "batch": self.batch, "block": self.width, "vocab": self.vocab}
+
+    def cpu_baseline(self, threads):
+        from oracle import verify as ov
+        from longspark_amd import workloads
+        b = 2
+        d = workloads.stochastic_inputs(b, self.width, self.vocab, seed=7, **self.cfg)
+        p = d["params"]
+        add, scale = ov.penalty_tables(list(d["history"]), self.vocab, d["repetition"], d["presence"], d["frequency"])
+        torch.set_num_threads(threads)
+
+        def run():
+            ov.verify_sample(logits=d["logits"], candidates=d["candidates"].long(), draft_logits=d["draft_logits"],
+                             draft_token_probs=d["draft_token_probs"], uniforms=d["uniforms"],
+                             final_uniforms=d["final_uniforms"], temperatures=p.temperatures, top_ks=p.top_ks,
+                             top_ps=p.top_ps, min_ps=p.min_ps, additive=add, scaling=scale,
+                             draft_top_ks=p.top_ks, draft_top_ps=p.top_ps, draft_min_ps=p.min_ps)
+        med, n = time_cpu(run)
+        return {"rows_per_s": b * self.width / med, "threads": threads,
+                "sample": f"B={b} x K={self.width} x V={self.vocab} (same sampling config), oracle torch-CPU path "
+                          f"(penalties, target distribution, acceptance, residual draw), median of {n} runs"}
+
+
+WORKLOADS = {w.name: w for w in (GreedyVerify, StochasticVerify)}
+DEFAULT_WORKLOAD = "verify_sample"
 
 
 def main(argv=None):
@@ -130,6 +233,8 @@ def main(argv=None):
     for _ in range(args.warmup):
         wl.step()
     torch.cuda.synchronize()
+    if hasattr(wl, "arm_timing"):
+        wl.arm_timing(args.steps)
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
@@ -140,9 +245,12 @@ def main(argv=None):
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_per_step = wall / args.steps * 1e3
-    kernel_ms = start.elapsed_time(end) / args.steps
+    step_gpu_ms = start.elapsed_time(end) / args.steps
     value = wl.rows / (ms_per_step / 1e3)
-    achieved = wl.bytes / (kernel_ms / 1e3) / 1e9
+    kernels = wl.kernel_times_ms() if hasattr(wl, "kernel_times_ms") else {wl.kernel: step_gpu_ms}
+    kernel_ms = kernels[wl.kernel]
+    kernel_bytes = getattr(wl, "kernel_bytes", wl.bytes)
+    achieved = kernel_bytes / (kernel_ms / 1e3) / 1e9
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -169,7 +277,10 @@ def main(argv=None):
         "config": wl.config(),
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel": wl.kernel,
-                     "kernel_avg_us": kernel_ms * 1e3, "algorithmic_bytes": wl.bytes},
+                     "kernel_avg_us": kernel_ms * 1e3, "algorithmic_bytes": kernel_bytes},
+        "step": {"gpu_us": step_gpu_ms * 1e3, "algorithmic_bytes": wl.bytes,
+                 "gbs": wl.bytes / (step_gpu_ms / 1e3) / 1e9,
+                 "kernels_us": {k: v * 1e3 for k, v in kernels.items()}},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -115,13 +115,16 @@ LS_API int ls_verify_greedy(const void* logits, int32_t logits_dtype, int64_t lo
  *   history_lens (int32 [batch], may be NULL = history_cap) entries per row.
  *   Ids outside [0, vocab) are ignored.
  * words_stride >= ceil(vocab/32); add_stride >= history_cap.
- * distinct (int32 [batch], may be NULL) receives the number of present tokens.
+ * distinct (int32 [batch], may be NULL) receives the number of present tokens;
+ * nonpositive (int32 [batch], may be NULL) receives 1 where every additive
+ * value is <= 0 (frequency and presence >= 0), else 0.
  * Limit: 8*ceil(vocab/32) + 4*history_cap <= 64 KiB.
  * ------------------------------------------------------------------------- */
 LS_API int ls_penalty_tables(const int32_t* history, int64_t history_stride, const int32_t* history_lens,
                              int64_t batch, int32_t history_cap, int64_t vocab, const float* frequency,
                              const float* presence, uint32_t* bits, uint32_t* rank, int64_t words_stride,
-                             float* add, int64_t add_stride, int32_t* distinct, void* stream);
+                             float* add, int64_t add_stride, int32_t* distinct, int32_t* nonpositive,
+                             void* stream);
 
 /* ---------------------------------------------------------------------------
  * In-place logit adjustment of [rows, vocab] logits: penalties (tables from
@@ -168,8 +171,11 @@ LS_API int ls_adjust_logits(void* logits, int32_t logits_dtype, int64_t row_stri
  *   top_ks (int32, >= vocab disables; NULL = disabled), top_ps (>= 1 disables),
  *   min_ps (<= 0 disables).  max_top_k: host upper bound of top_ks (0 = 1024);
  *   top-k above 1024 is not supported.
- * Penalties (optional): tables from ls_penalty_tables, pen_repetition [batch]
- *   (NULL = 1); pen_verify_quirk as in ls_adjust_logits.
+ * Penalties (optional): tables from ls_penalty_tables (pen_add NULL = no
+ *   additive penalties), pen_repetition [batch] (NULL = 1); pen_verify_quirk
+ *   as in ls_adjust_logits; pen_nonpositive [batch] (may be NULL) lets top-k
+ *   rows whose penalties never raise a logit (repetition >= 1, additive <= 0)
+ *   filter on raw logits and transform only their candidates.
  * vocab_mask (optional): int32 words, mask_row_stride >= ceil(vocab/32);
  *   mask_per_request = 1: row b, else row r.
  * Draft: q_mode 0 -- draft_token_probs [batch, width-1] fp32 (q of each drafted
@@ -210,6 +216,7 @@ typedef struct {
   int64_t pen_add_stride;
   const float* pen_repetition;
   int32_t pen_verify_quirk;
+  const int32_t* pen_nonpositive; /* [batch] from ls_penalty_tables, may be NULL */
   const int32_t* vocab_mask;
   int64_t mask_row_stride;
   int32_t mask_per_request;
@@ -231,6 +238,10 @@ typedef struct {
   int64_t* bonus;
   float* p_cand_out;
   int32_t* status;
+  /* Optional timing: NULL, or 4 hipEvent_t handles recorded on the stream
+   * before the target scan, after it, before the resolve kernel and after it
+   * (the middle interval holds the fallback and draft-scan kernels). */
+  void* const* timing_events;
 } ls_verify_sample_args;
 
 LS_API int ls_verify_sample_workspace(int64_t batch, int32_t width, int64_t vocab, int32_t max_top_k,

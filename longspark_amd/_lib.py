@@ -46,13 +46,14 @@ class VerifySampleArgs(ctypes.Structure):
         ("batch", I64), ("width", I32), ("vocab", I64),
         ("temperatures", P), ("top_ks", P), ("top_ps", P), ("min_ps", P), ("max_top_k", I32),
         ("pen_bits", P), ("pen_rank", P), ("pen_words_stride", I64), ("pen_add", P), ("pen_add_stride", I64),
-        ("pen_repetition", P), ("pen_verify_quirk", I32),
+        ("pen_repetition", P), ("pen_verify_quirk", I32), ("pen_nonpositive", P),
         ("vocab_mask", P), ("mask_row_stride", I64), ("mask_per_request", I32),
         ("q_mode", I32), ("draft_token_probs", P), ("dtp_stride_b", I64),
         ("draft", P), ("draft_dtype", I32), ("draft_stride_b", I64), ("draft_stride_k", I64),
         ("draft_temperatures", P), ("draft_top_ks", P), ("draft_top_ps", P), ("draft_min_ps", P),
         ("uniforms", P), ("uniform_stride_b", I64), ("final_uniforms", P),
         ("accept_lens", P), ("bonus", P), ("p_cand_out", P), ("status", P),
+        ("timing_events", P),
     ]
 
 
@@ -63,7 +64,7 @@ _SIGNATURES = {
     "ls_verify_greedy_workspace": (I32, [I64, I32, I64, P, P]),
     "ls_verify_greedy": (I32, [P, I32, I64, P, I32, I64, I64, I32, I64, I32, I64, P, P, P, P, P,
                                P, U64, P, U64, P]),
-    "ls_penalty_tables": (I32, [P, I64, P, I64, I32, I64, P, P, P, P, I64, P, I64, P, P]),
+    "ls_penalty_tables": (I32, [P, I64, P, I64, I32, I64, P, P, P, P, I64, P, I64, P, P, P]),
     "ls_adjust_logits": (I32, [P, I32, I64, I64, I64, I32, P, P, I64, P, I64, P, I32, P, I64, I32, I64, P]),
     "ls_verify_sample_workspace": (I32, [I64, I32, I64, I32, P, P]),
     "ls_verify_sample": (I32, [ctypes.POINTER(VerifySampleArgs), P, U64, P, U64, P]),

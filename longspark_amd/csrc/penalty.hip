@@ -24,7 +24,8 @@ __global__ __launch_bounds__(kPT) void penalty_tables_kernel(
     const int32_t* __restrict__ hist, int64_t hist_stride, const int32_t* __restrict__ hist_lens, int hist_cap,
     int64_t vocab, int words, const float* __restrict__ freq, const float* __restrict__ pres,
     uint32_t* __restrict__ bits_out, uint32_t* __restrict__ rank_out, int64_t words_stride,
-    float* __restrict__ add_out, int64_t add_stride, int32_t* __restrict__ distinct_out) {
+    float* __restrict__ add_out, int64_t add_stride, int32_t* __restrict__ distinct_out,
+    int32_t* __restrict__ nonpos_out) {
   extern __shared__ uint32_t lds[];
   uint32_t* bits = lds;              // [words]
   uint32_t* rank = lds + words;      // [words]
@@ -90,6 +91,8 @@ __global__ __launch_bounds__(kPT) void penalty_tables_kernel(
     ao[r] = a;
   }
   if (tid == 0 && distinct_out) distinct_out[b] = static_cast<int32_t>(distinct);
+  // Every additive value is <= 0 exactly when frequency and presence are >= 0.
+  if (tid == 0 && nonpos_out) nonpos_out[b] = (f >= 0.f && p >= 0.f) ? 1 : 0;
 }
 
 // In-place adjustment of [rows, V] logits: penalties then mask (true order),
@@ -105,7 +108,7 @@ __global__ __launch_bounds__(kPT) void adjust_logits_kernel(
   rs::XForm f;
   f.pbits = pbits ? pbits + b * pwords_stride : nullptr;
   f.prank = pbits ? prank + b * pwords_stride : nullptr;
-  f.padd = pbits ? padd + b * padd_stride : nullptr;
+  f.padd = (pbits && padd) ? padd + b * padd_stride : nullptr;
   f.rep = rep ? rep[b] : 1.f;
   f.quirk = quirk;
   const int64_t mrow = mask_rows_per_request > 1 ? b : row;
@@ -126,7 +129,8 @@ __global__ __launch_bounds__(kPT) void adjust_logits_kernel(
 extern "C" int ls_penalty_tables(const int32_t* history, int64_t history_stride, const int32_t* history_lens,
                                  int64_t batch, int32_t history_cap, int64_t vocab, const float* frequency,
                                  const float* presence, uint32_t* bits, uint32_t* rank, int64_t words_stride,
-                                 float* add, int64_t add_stride, int32_t* distinct, void* stream) {
+                                 float* add, int64_t add_stride, int32_t* distinct, int32_t* nonpositive,
+                                 void* stream) {
   using namespace ls;
   LS_CHECK(batch > 0 && vocab > 0 && history_cap >= 0, LS_ERR_SHAPE, "ls_penalty_tables: bad sizes");
   const int64_t words = (vocab + 31) / 32;
@@ -140,7 +144,7 @@ extern "C" int ls_penalty_tables(const int32_t* history, int64_t history_stride,
            (long long)vocab, history_cap);
   penalty_tables_kernel<<<dim3(static_cast<unsigned>(batch)), kPT, lds, static_cast<hipStream_t>(stream)>>>(
       history, history_stride, history_lens, history_cap, vocab, static_cast<int>(words), frequency, presence,
-      bits, rank, words_stride, add, add_stride, distinct);
+      bits, rank, words_stride, add, add_stride, distinct, nonpositive);
   LS_LAUNCH_CHECK();
   return LS_OK;
 }
@@ -156,7 +160,7 @@ extern "C" int ls_adjust_logits(void* logits, int32_t logits_dtype, int64_t row_
            "ls_adjust_logits: rows must be a positive multiple of rows_per_request");
   LS_CHECK(row_stride >= vocab, LS_ERR_SHAPE, "ls_adjust_logits: row stride < vocab");
   LS_CHECK(rows <= 65535, LS_ERR_SHAPE, "ls_adjust_logits: at most 65535 rows per call");
-  LS_CHECK(!pen_bits || (pen_rank && pen_add), LS_ERR_VALUE, "ls_adjust_logits: incomplete penalty tables");
+  LS_CHECK(!pen_bits || pen_rank, LS_ERR_VALUE, "ls_adjust_logits: penalty bitmap without ranks");
   LS_CHECK(!vocab_mask || (mask_rows_per_request == 1 || mask_rows_per_request == rows_per_request),
            LS_ERR_VALUE, "ls_adjust_logits: mask must be per row or per request");
   LS_CHECK(!vocab_mask || (mask_words > 0 && mask_words * 32 >= 1 && mask_stride >= mask_words), LS_ERR_SHAPE,

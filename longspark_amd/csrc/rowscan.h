@@ -56,7 +56,7 @@ __device__ __forceinline__ int row_mode(const Params& p, int64_t vocab) {
 struct XForm {
   const uint32_t* pbits;  // presence bitmap of the request's history [W32]
   const uint32_t* prank;  // exclusive popcount prefix per bitmap word [W32]
-  const float* padd;      // additive penalty per present token, by rank
+  const float* padd;      // additive penalty per present token, by rank (null: all zero)
   float rep;              // repetition scaling of present tokens
   int quirk;              // 1: verify-path quirk (penalty built on zeros)
   const uint32_t* mbits;  // vocabulary mask row [W32] (bit 0 -> -inf)
@@ -79,7 +79,7 @@ __device__ __forceinline__ float transform1(const XForm& f, float x, int64_t v) 
     const uint32_t word = f.pbits[w];
     if (word & bit) {
       const uint32_t rank = f.prank[w] + __popc(word & (bit - 1u));
-      x = penalise(x, f.padd[rank], f.rep, f.quirk);
+      x = penalise(x, f.padd ? f.padd[rank] : 0.f, f.rep, f.quirk);
     }
   }
   if (f.mbits && !(f.mbits[w] & bit)) x = -INFINITY;
@@ -101,7 +101,7 @@ __device__ __forceinline__ void transform_vec(const XForm& f, float* x, int64_t 
 #pragma unroll
       for (int k = 0; k < P; ++k) {
         if ((hit >> k) & 1u) {
-          x[k] = penalise(x[k], f.padd[rank], f.rep, f.quirk);
+          x[k] = penalise(x[k], f.padd ? f.padd[rank] : 0.f, f.rep, f.quirk);
           ++rank;
         }
       }
@@ -142,6 +142,7 @@ struct Shared {
   float tau_x;      // current x-domain append threshold
   float wg_max_x;   // workgroup running maximum of x (filter mode)
   int overflow;
+  int ntrans;       // raw-filter scan: entries [0, ntrans) hold transformed values
 };
 
 // Wave-aggregated append of the elements of x[0..P) that are >= tau.

@@ -31,7 +31,7 @@ struct RowRec {
   float p_cand;   // probability of the drafted token this row verifies
   int n;          // support entries (-1: dense support)
   int flags;
-  int pad;
+  int why;        // diagnostics: Why bits of a row resolved by the fallback
   uint64_t last;  // key of the last support entry
 };
 
@@ -57,6 +57,7 @@ struct Args {
   int64_t pas;
   const float* prep;
   int quirk;
+  const int32_t* pnonpos;
   const uint32_t* mask;
   int64_t mrs;
   int mask_per_request;
@@ -92,6 +93,9 @@ struct Args {
   uint64_t* pubs_t;   // [B*K, S_t, 2]
   uint64_t* pub_d;    // [B, kNBuf]
   uint64_t* pubs_d;   // [B, S_d, 2]
+  uint32_t* list_cnt;  // counters [2]: rows waiting for the exact fallback (target, draft)
+  int32_t* list_t;     // [B*K]
+  int32_t* list_d;     // [B]
   int s_t, s_d;
 };
 
@@ -108,12 +112,47 @@ struct ScanOut {
   float z;    // sum exp((x - mz) / T) (thread)
 };
 
+constexpr int kMaint = 4;  // steps between maintenance points
+
+// Why a row went to the exact fallback (kept in RowRec::why for diagnostics).
+enum Why : int {
+  kWhyLost = 1,       // more appends than the buffer holds between maintenance points
+  kWhyTies = 2,       // top-k compaction left more than the trigger (ties)
+  kWhyFilter = 4,     // min-p / top-p candidates exceed the buffer
+  kWhyMerge = 8,      // slice hand-off could not hold the candidates
+  kWhySort = 16,      // more than 2048 candidates at finalisation
+  kWhyNucleus = 32,   // top-p nucleus extends past the candidates
+  kWhyCap = 64,       // support larger than a record holds
+  kWhyExact = 256,    // record written by the fallback
+};
+
+// k-th largest (ties counted) of the kT values v (one per thread), k <= kT.
+__device__ __noinline__ float kth_largest_of_block(Shared& sh, float v, int k) {
+  float* vals = reinterpret_cast<float*>(sh.hist);  // kT floats
+  __shared__ float res;
+  const int tid = threadIdx.x;
+  vals[tid] = v;
+  if (tid == 0) res = -INFINITY;
+  __syncthreads();
+  int gt = 0, ge = 0;
+  for (int j = 0; j < kT; ++j) {
+    const float w = vals[j];
+    gt += w > v;
+    ge += w >= v;
+  }
+  if (gt < k && k <= ge) res = v;  // every writer holds the same value
+  __syncthreads();
+  const float r = res;
+  __syncthreads();
+  return r;
+}
+
 // Compaction of an over-full candidate buffer (all threads; rare).
 __device__ __noinline__ void compact_slow(Shared& sh, int mode, int k, float t, float off_s) {
   const int count = sh.count;
   if (count > kNBuf) {
     __syncthreads();
-    if (threadIdx.x == 0) { sh.overflow = 1; sh.tau_x = INFINITY; }
+    if (threadIdx.x == 0) { sh.overflow |= kWhyLost; sh.tau_x = INFINITY; }
     __syncthreads();
     return;
   }
@@ -121,13 +160,13 @@ __device__ __noinline__ void compact_slow(Shared& sh, int mode, int k, float t, 
     const uint32_t thr = select_kth_s(sh, count, k);
     compact_ge(sh, thr);
     if (threadIdx.x == 0) {
-      if (sh.count > kNBHi) { sh.overflow = 1; sh.tau_x = INFINITY; }
+      if (sh.count > kNBHi) { sh.overflow |= kWhyTies; sh.tau_x = INFINITY; }
       else sh.tau_x = x_threshold(unordered_f32(thr), t);
     }
   } else {
     const float wmx = unordered_f32(*reinterpret_cast<unsigned*>(&sh.wg_max_x));
     compact_ge(sh, ordered_f32(wmx / t + off_s));
-    if (threadIdx.x == 0 && sh.count > kNBHi) { sh.overflow = 1; sh.tau_x = INFINITY; }
+    if (threadIdx.x == 0 && sh.count > kNBHi) { sh.overflow |= kWhyFilter; sh.tau_x = INFINITY; }
   }
   __syncthreads();
 }
@@ -153,12 +192,64 @@ __device__ __forceinline__ float maintain(Shared& sh, int mode, int k, float t, 
   return tau;
 }
 
+// Ring slot: one 16-byte logits vector plus the 32-token words that cover it
+// (presence bitmap, its popcount rank base, vocabulary mask), all prefetched
+// four steps ahead so the per-element transform never waits on a load.
+struct Slot {
+  uint4 v;
+  uint32_t pb, pr, mb;
+};
+
+template <int P>
+__device__ __forceinline__ void load_slot(Slot& s, const uint4* vp, int64_t i, int64_t nfull, const XForm& f,
+                                          int64_t b) {
+  if (i < nfull) {
+    s.v = load16_stream(vp + i);
+    const int64_t w = (b + i * P) >> 5;
+    if (f.pbits) {
+      s.pb = f.pbits[w];
+      s.pr = f.prank[w];
+    }
+    if (f.mbits) s.mb = f.mbits[w];
+  }
+}
+
+// Transform P consecutive elements starting at e0 given their prefetched words.
+template <int P>
+__device__ __forceinline__ void transform_words(const XForm& f, float* x, int64_t e0, const Slot& s) {
+  const int sh = static_cast<int>(e0 & 31);
+  constexpr uint32_t lanes = (1u << P) - 1u;
+  if (f.pbits) {
+    const uint32_t hit = (s.pb >> sh) & lanes;
+    if (hit) {
+      uint32_t rank = s.pr + __popc(s.pb & ((1u << sh) - 1u));
+#pragma unroll
+      for (int k = 0; k < P; ++k) {
+        if ((hit >> k) & 1u) {
+          const float a = f.padd ? f.padd[rank] : 0.f;
+          x[k] = penalise(x[k], a, f.rep, f.quirk);
+          ++rank;
+        }
+      }
+    }
+  }
+  if (f.mbits) {
+    const uint32_t m = (s.mb >> sh) & lanes;
+    if (m != lanes) {
+#pragma unroll
+      for (int k = 0; k < P; ++k)
+        if (!((m >> k) & 1u)) x[k] = -INFINITY;
+    }
+  }
+}
+
 template <typename Tag, bool kVec>
 __device__ ScanOut scan_range(Shared& sh, const typename Tag::storage* row, int64_t b, int64_t e,
                               const XForm& f, float t, int mode, int k, float off_s) {
   using S = typename Tag::storage;
   constexpr int P = Tag::kPerVec;
   const bool need_z = mode != kModeTopK;
+  const bool xform = f.pbits || f.mbits;
   const float c2 = 1.4426950408889634f / t;
   const float off_x = (mode == kModeFilter) ? off_s * t : -INFINITY;
   const int tid = threadIdx.x;
@@ -168,38 +259,67 @@ __device__ ScanOut scan_range(Shared& sh, const typename Tag::storage* row, int6
   const int64_t nfull = kVec ? (e - b) / P : 0;    // vectors loadable with 16-byte loads
   const int64_t steps = (nvv + kT - 1) / kT;
   const uint4* vp = reinterpret_cast<const uint4*>(row + b);
-  // Four 16-byte loads in flight per thread, rotated through a ring.
-  uint4 r0 = {}, r1 = {}, r2 = {}, r3 = {};
-  if (tid < nfull) r0 = load16_stream(vp + tid);
-  if (kT + tid < nfull) r1 = load16_stream(vp + kT + tid);
-  if (2 * kT + tid < nfull) r2 = load16_stream(vp + 2 * kT + tid);
-  if (3 * kT + tid < nfull) r3 = load16_stream(vp + 3 * kT + tid);
-  for (int64_t st = 0; st < steps; ++st) {
+  // Four slots in flight per thread, rotated through a ring.
+  Slot r0 = {}, r1 = {}, r2 = {}, r3 = {};
+  load_slot<P>(r0, vp, tid, nfull, f, b);
+  load_slot<P>(r1, vp, kT + tid, nfull, f, b);
+  load_slot<P>(r2, vp, 2 * kT + tid, nfull, f, b);
+  load_slot<P>(r3, vp, 3 * kT + tid, nfull, f, b);
+  int64_t st = 0;
+  if (mode == kModeTopK && k <= kT && nfull >= 8 * kT) {
+    // Prologue: the first four vectors of every thread give kT per-thread
+    // maxima; their k-th largest is a lower bound of the row's k-th largest
+    // value (k distinct elements reach it), so it can start the threshold.
+    float lm = -INFINITY;
+#pragma unroll 1
+    for (int d = 0; d < 4; ++d) {
+      const Slot& s = d == 0 ? r0 : d == 1 ? r1 : d == 2 ? r2 : r3;
+      float x[P];
+      unpack16<Tag>(s.v, x);
+      if (xform) transform_words<P>(f, x, b + (static_cast<int64_t>(d) * kT + tid) * P, s);
+#pragma unroll
+      for (int q = 0; q < P; ++q) lm = fmaxf(lm, x[q]);
+    }
+    float t0 = kth_largest_of_block(sh, lm, k);
+    t0 = t0 - fabsf(t0) * 9.5367431640625e-07f - 1e-30f;
+    tau = fmaxf(tau, t0);
+    if (tid == 0) sh.tau_x = tau;  // read again at the next maintenance point
+    o.mx = lm;
+#pragma unroll 1
+    for (int d = 0; d < 4; ++d) {
+      const Slot& s = d == 0 ? r0 : d == 1 ? r1 : d == 2 ? r2 : r3;
+      float x[P];
+      unpack16<Tag>(s.v, x);
+      const int64_t e0 = b + (static_cast<int64_t>(d) * kT + tid) * P;
+      if (xform) transform_words<P>(f, x, e0, s);
+      float vm = x[0];
+#pragma unroll
+      for (int q = 1; q < P; ++q) vm = fmaxf(vm, x[q]);
+      if (__ballot(vm >= tau)) append_vec<P>(sh, x, tau, e0, t);
+    }
+    load_slot<P>(r0, vp, 4 * kT + tid, nfull, f, b);
+    load_slot<P>(r1, vp, 5 * kT + tid, nfull, f, b);
+    load_slot<P>(r2, vp, 6 * kT + tid, nfull, f, b);
+    load_slot<P>(r3, vp, 7 * kT + tid, nfull, f, b);
+    st = 4;
+  }
+  for (; st < steps; ++st) {
     const int64_t i = st * kT + tid;
-    const uint4 cur = r0;
+    const Slot cur = r0;
     r0 = r1;
     r1 = r2;
     r2 = r3;
-    const int64_t inext = i + 4 * kT;
-    if (inext < nfull) r3 = load16_stream(vp + inext);
+    load_slot<P>(r3, vp, i + 4 * kT, nfull, f, b);
     float x[P];
+    const int64_t e0 = b + i * P;
     if (i < nfull) {
-      unpack16<Tag>(cur, x);
+      unpack16<Tag>(cur.v, x);
+      if (xform) transform_words<P>(f, x, e0, cur);
     } else {
 #pragma unroll
       for (int q = 0; q < P; ++q) {
-        const int64_t v = b + i * P + q;
-        x[q] = (i < nvv && v < e) ? to_f32<S>(row[v]) : -INFINITY;
-      }
-    }
-    const int64_t e0 = b + i * P;
-    if (i < nvv && (f.pbits || f.mbits)) {
-      if (i < nfull) {
-        transform_vec<P>(f, x, e0);
-      } else {
-#pragma unroll
-        for (int q = 0; q < P; ++q)
-          if (e0 + q < e) x[q] = transform1(f, x[q], e0 + q);
+        const int64_t v = e0 + q;
+        x[q] = (i < nvv && v < e) ? transform1(f, to_f32<S>(row[v]), v) : -INFINITY;
       }
     }
     float vmax = x[0];
@@ -216,9 +336,221 @@ __device__ ScanOut scan_range(Shared& sh, const typename Tag::storage* row, int6
     o.mx = fmaxf(o.mx, vmax);
     const float tau_eff = fmaxf(tau, o.mx + off_x);
     if (__ballot(vmax >= tau_eff)) append_vec<P>(sh, x, tau_eff, e0, t);
-    tau = maintain(sh, mode, k, t, off_s, o.mx);
+    // Maintenance every kMaint steps (and at the last): between two points at
+    // most kMaint * kT * P entries arrive; any beyond the buffer are dropped and
+    // flagged, which sends the row to the exact fallback.
+    if ((st & (kMaint - 1)) == kMaint - 1 || st + 1 == steps) tau = maintain(sh, mode, k, t, off_s, o.mx);
   }
   return o;
+}
+
+// ----------------------------------------------------- raw-filter top-k ---
+//
+// Top-k rows whose transform never raises a logit (no penalties, or
+// repetition >= 1 with additive penalties <= 0; the mask only lowers values to
+// -inf) are scanned on the raw logits: every element whose transformed value
+// can reach the threshold has a raw value that does, so filtering raw values
+// keeps every candidate.  Candidates are buffered with raw keys and
+// transformed in bulk when the buffer is compacted and at the end; thresholds
+// always come from transformed values.  Keys here are in the logit (x) domain
+// and become scaled-logit (x / T) keys at the end of the slice.
+
+constexpr int kRawMaint = 16;  // steps between maintenance points
+
+__device__ __forceinline__ float x_lower(float x) {
+  return x - fabsf(x) * 9.5367431640625e-07f /* 2^-20 */ - 1e-30f;
+}
+
+// Wave-aggregated append of raw keys (one LDS atomic per wave).  All 64
+// lanes of the wave must call it.
+template <int P>
+__device__ __forceinline__ void append_raw(Shared& sh, const float* x, float tau, int64_t e0) {
+  uint32_t pm = 0;
+#pragma unroll
+  for (int q = 0; q < P; ++q) pm |= (x[q] >= tau ? 1u : 0u) << q;
+  const int cnt = __popc(pm);
+  const int lane = threadIdx.x & (kWave - 1);
+  int incl = cnt;
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const int v = __shfl_up(incl, o, kWave);
+    if (lane >= o) incl += v;
+  }
+  const int total = __shfl(incl, kWave - 1, kWave);
+  int base = 0;
+  if (lane == 0) base = atomicAdd(&sh.count, total);
+  base = __shfl(base, 0, kWave);
+  int pos = base + incl - cnt;
+#pragma unroll
+  for (int q = 0; q < P; ++q) {
+    if ((pm >> q) & 1u) {
+      if (pos < kNBuf) sh.buf[pos] = cand_key(x[q], static_cast<int>(e0 + q));
+      ++pos;
+    }
+  }
+}
+
+// Transform the buffered entries appended since the last transform (all threads).
+__device__ __noinline__ void transform_pending(Shared& sh, const XForm& f) {
+  const int n = min(sh.count, kNBuf);
+  if (f.pbits || f.mbits) {
+    for (int i = sh.ntrans + static_cast<int>(threadIdx.x); i < n; i += kT) {
+      const uint64_t key = sh.buf[i];
+      const int idx = key_idx(key);
+      sh.buf[i] = cand_key(transform1(f, key_s(key), idx), idx);
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) sh.ntrans = n;
+  __syncthreads();
+}
+
+// Transform, select the k-th largest transformed value and keep the entries
+// within the rounding margin of it (all threads).  Returns the new raw
+// threshold.
+__device__ __noinline__ float compact_raw(Shared& sh, const XForm& f, int k) {
+  transform_pending(sh, f);
+  const int n = min(sh.count, kNBuf);
+  if (n <= k) return -FLT_MAX;
+  const float xk = unordered_f32(select_kth_s(sh, n, k));
+  const float thr = x_lower(xk);
+  compact_ge(sh, ordered_f32(thr));
+  if (threadIdx.x == 0) sh.ntrans = sh.count;
+  __syncthreads();
+  return thr;
+}
+
+__device__ __forceinline__ float maintain_raw(Shared& sh, const XForm& f, int k, int trigger) {
+  __syncthreads();
+  const int count = sh.count;
+  const int ovf = sh.overflow;
+  __syncthreads();
+  if (ovf) return INFINITY;
+  if (count > kNBuf) {
+    if (threadIdx.x == 0) { sh.overflow |= kWhyLost; sh.tau_x = INFINITY; }
+    __syncthreads();
+    return INFINITY;
+  }
+  if (count > trigger) {
+    const float thr = compact_raw(sh, f, k);
+    if (threadIdx.x == 0) {
+      if (sh.count > kNBHi) { sh.overflow |= kWhyTies; sh.tau_x = INFINITY; }
+      else sh.tau_x = fmaxf(sh.tau_x, thr);
+    }
+    __syncthreads();
+  }
+  return sh.tau_x;
+}
+
+template <typename Tag, bool kVec>
+__device__ ScanOut scan_topk_raw(Shared& sh, const typename Tag::storage* row, int64_t b, int64_t e,
+                                 const XForm& f, int k) {
+  using S = typename Tag::storage;
+  constexpr int P = Tag::kPerVec;
+  const int tid = threadIdx.x;
+  const int trigger = min(kNBHi, max(2 * k + 64, 256));
+  // Larger k admits more candidates per step: compact more often.
+  const int maint_mask = k <= 64 ? kRawMaint - 1 : (k <= 256 ? 3 : 0);
+  ScanOut o{-FLT_MAX, -FLT_MAX, 0.f};
+  float tau = sh.tau_x;
+  const int64_t nvv = (e - b + P - 1) / P;
+  const int64_t nfull = kVec ? (e - b) / P : 0;
+  const int64_t steps = (nvv + kT - 1) / kT;
+  const uint4* vp = reinterpret_cast<const uint4*>(row + b);
+  uint4 r0 = {}, r1 = {}, r2 = {}, r3 = {};
+  if (tid < nfull) r0 = load16_stream(vp + tid);
+  if (kT + tid < nfull) r1 = load16_stream(vp + kT + tid);
+  if (2 * kT + tid < nfull) r2 = load16_stream(vp + 2 * kT + tid);
+  if (3 * kT + tid < nfull) r3 = load16_stream(vp + 3 * kT + tid);
+  int64_t st = 0;
+  if (k <= kT && nfull >= 8 * kT) {
+    // Prologue: the k-th largest of the kT per-thread maxima of the first
+    // four transformed vectors is a lower bound of the row's k-th largest
+    // transformed value.
+    float lm = -INFINITY, rm = -INFINITY;
+#pragma unroll 1
+    for (int d = 0; d < 4; ++d) {
+      const uint4 v = d == 0 ? r0 : d == 1 ? r1 : d == 2 ? r2 : r3;
+      float x[P];
+      unpack16<Tag>(v, x);
+#pragma unroll
+      for (int q = 0; q < P; ++q) rm = fmaxf(rm, x[q]);
+      if (f.pbits || f.mbits) transform_vec<P>(f, x, b + (static_cast<int64_t>(d) * kT + tid) * P);
+#pragma unroll
+      for (int q = 0; q < P; ++q) lm = fmaxf(lm, x[q]);
+    }
+    tau = fmaxf(tau, x_lower(kth_largest_of_block(sh, lm, k)));
+    if (tid == 0) sh.tau_x = tau;
+    o.mx = rm;
+#pragma unroll 1
+    for (int d = 0; d < 4; ++d) {
+      const uint4 v = d == 0 ? r0 : d == 1 ? r1 : d == 2 ? r2 : r3;
+      float x[P];
+      unpack16<Tag>(v, x);
+      float vm = x[0];
+#pragma unroll
+      for (int q = 1; q < P; ++q) vm = fmaxf(vm, x[q]);
+      if (__ballot(vm >= tau)) append_raw<P>(sh, x, tau, b + (static_cast<int64_t>(d) * kT + tid) * P);
+    }
+    r0 = load16_stream(vp + 4 * kT + tid);
+    r1 = load16_stream(vp + 5 * kT + tid);
+    r2 = load16_stream(vp + 6 * kT + tid);
+    r3 = load16_stream(vp + 7 * kT + tid);
+    st = 4;
+  }
+  for (; st < steps; ++st) {
+    const int64_t i = st * kT + tid;
+    const uint4 cur = r0;
+    r0 = r1;
+    r1 = r2;
+    r2 = r3;
+    if (i + 4 * kT < nfull) r3 = load16_stream(vp + i + 4 * kT);
+    float x[P];
+    const int64_t e0 = b + i * P;
+    if (i < nfull) {
+      unpack16<Tag>(cur, x);
+    } else {
+#pragma unroll
+      for (int q = 0; q < P; ++q) {
+        const int64_t v = e0 + q;
+        x[q] = (i < nvv && v < e) ? to_f32<S>(row[v]) : -INFINITY;
+      }
+    }
+    float vmax = x[0];
+#pragma unroll
+    for (int q = 1; q < P; ++q) vmax = fmaxf(vmax, x[q]);
+    o.mx = fmaxf(o.mx, vmax);
+    if (__ballot(vmax >= tau)) append_raw<P>(sh, x, tau, e0);
+    if ((st & maint_mask) == maint_mask || st + 1 == steps) tau = maintain_raw(sh, f, k, trigger);
+  }
+  return o;
+}
+
+// End of a raw-filter slice: transform what is pending, keep the top k within
+// the rounding margin, and re-key the survivors by scaled logit x / T.
+__device__ __noinline__ ScanOut finish_topk_raw(Shared& sh, const ScanOut& o, const XForm& f, int k, float t) {
+  ScanOut r;
+  r.mx = block_max(sh, o.mx);  // raw maximum: an upper bound of the transformed one
+  r.mz = r.mx;
+  r.z = 0.f;
+  if (!sh.overflow) {
+    transform_pending(sh, f);
+    const int n = min(sh.count, kNBuf);
+    if (n > k) compact_raw(sh, f, k);
+    const int m = min(sh.count, kNBuf);
+    for (int i = threadIdx.x; i < m; i += kT) {
+      const uint64_t key = sh.buf[i];
+      const int idx = key_idx(key);
+      sh.buf[i] = cand_key(key_s(key) / t, idx);
+    }
+  }
+  __syncthreads();
+  return r;
+}
+
+__device__ __forceinline__ bool raw_filter_ok(const XForm& f, const int32_t* nonpos, int64_t b) {
+  if (!f.pbits) return true;
+  return f.rep >= 1.0f && (!f.padd || (nonpos && nonpos[b]));
 }
 
 // After the scan of a slice: final compaction of the slice's candidates and
@@ -488,17 +820,17 @@ __device__ __noinline__ Exact exact_support(Shared& sh, const typename Tag::stor
 // hold the support, from the row itself) and write the row record.  `cand_x`
 // is the transformed logit of the drafted token this row verifies.  All
 // threads.
-template <typename Tag>
 __device__ __noinline__ void finalize_row(Shared& sh, const ScanOut& st, const Params& p, int mode, int64_t vocab,
-                                          const typename Tag::storage* row, const XForm& f, RowRec* rec,
-                                          int32_t* sidx, float* sp, int cand_tok, float cand_x) {
+                                          RowRec* rec, int32_t* sidx, float* sp, int cand_tok, float cand_x,
+                                          uint32_t* list_cnt, int32_t* list, int32_t list_id) {
   const int tid = threadIdx.x;
   __shared__ float s_m, s_z;
-  __shared__ int s_n, s_flags;
+  __shared__ int s_n, s_flags, s_why;
   __shared__ uint64_t s_last;
   const float t = p.temperature;
   if (tid == 0) {
     s_flags = sh.overflow ? kFlagOverflow : 0;
+    s_why = sh.overflow;
     s_last = 0;
   }
   __syncthreads();
@@ -512,7 +844,7 @@ __device__ __noinline__ void finalize_row(Shared& sh, const ScanOut& st, const P
     }
   } else if (!s_flags) {
     if (n > 2048) {
-      if (tid == 0) s_flags |= kFlagOverflow;
+      if (tid == 0) { s_flags |= kFlagOverflow; s_why |= kWhySort; }
     } else {
       sort_desc(sh, n);
       if (mode == kModeTopK && n > p.top_k) n = p.top_k;
@@ -530,7 +862,7 @@ __device__ __noinline__ void finalize_row(Shared& sh, const ScanOut& st, const P
       if (p.top_p < 1.0f && n > 0) {
         n_f = first_excl_exceeds(sh, n, m, z1, p.top_p, &mass_all);
         if (mode == kModeFilter && p.min_p <= 0.f && n_f == n && mass_all <= p.top_p) {
-          if (tid == 0) s_flags |= kFlagOverflow;  // nucleus extends past the candidates
+          if (tid == 0) { s_flags |= kFlagOverflow; s_why |= kWhyNucleus; }  // nucleus open
         }
       }
       if (p.min_p > 0.f && n_f > 0) {
@@ -551,7 +883,7 @@ __device__ __noinline__ void finalize_row(Shared& sh, const ScanOut& st, const P
         n_f = cut;
         __syncthreads();
       }
-      if (n_f > kCap && tid == 0) s_flags |= kFlagOverflow;
+      if (n_f > kCap && tid == 0) { s_flags |= kFlagOverflow; s_why |= kWhyCap; }
       float acc = 0.f;
       for (int i = tid; i < n_f; i += kT) acc += __expf(key_s(sh.buf[i]) - m);
       const float zf = block_sum(sh, acc);
@@ -566,24 +898,19 @@ __device__ __noinline__ void finalize_row(Shared& sh, const ScanOut& st, const P
   }
   __syncthreads();
   if (s_flags & kFlagOverflow) {
-    // Exact fallback from global memory.
-    const Exact ex = exact_support<Tag>(sh, row, vocab, f, p, mode, st.mx, st.z);
-    int n_f = ex.n;
-    if (n_f <= kCap) n_f = collect<Tag>(sh, row, vocab, f, t, ex.kcut);
+    // Resolved exactly by the fallback kernel; keep the row statistics.
     if (tid == 0) {
-      s_m = ex.m;
-      s_z = ex.z;
-      s_flags = 0;
-      if (ex.n <= kCap && n_f == ex.n) {
-        s_n = n_f;
-        s_last = n_f > 0 ? sh.buf[n_f - 1] : ~uint64_t(0);
-      } else {
-        s_n = -1;  // threshold support evaluated densely
-        s_last = ex.kcut;
-        s_flags = kFlagDense;
-      }
+      RowRec r{};
+      r.m = st.mx;  // x-domain maximum
+      r.z = st.z;   // dense normaliser (filter / dense modes)
+      r.flags = kFlagOverflow;
+      r.why = s_why;
+      *rec = r;
+      const uint32_t slot = atomic_add_u32(list_cnt, 1u);
+      list[slot] = list_id;
     }
     __syncthreads();
+    return;
   }
   if (s_n > 0) {
     for (int i = tid; i < s_n; i += kT) {
@@ -599,7 +926,7 @@ __device__ __noinline__ void finalize_row(Shared& sh, const ScanOut& st, const P
     r.z = s_z;
     r.n = s_n;
     r.flags = s_flags;
-    r.pad = 0;
+    r.why = 0;
     r.last = s_last;
     r.p_cand = 0.f;
     if (cand_tok >= 0) {
@@ -651,7 +978,7 @@ __device__ __noinline__ bool merge_slices(Shared& sh, ScanOut& st, int mode, int
       sz[s] = __uint_as_float(static_cast<uint32_t>(mz));
     }
     offs[slices] = total;
-    sh.overflow = bad || total > kNBuf;
+    sh.overflow = (bad || total > kNBuf) ? kWhyMerge : 0;
     sh.count = sh.overflow ? 0 : total;
     float gm = -FLT_MAX, z = 0.f;
     for (int s = 0; s < slices; ++s) gm = fmaxf(gm, smx[s]);
@@ -680,6 +1007,7 @@ __device__ __noinline__ bool merge_slices(Shared& sh, ScanOut& st, int mode, int
 __device__ void init_shared(Shared& sh, int mode) {
   if (threadIdx.x == 0) {
     sh.count = 0;
+    sh.ntrans = 0;
     sh.overflow = 0;
     sh.tau_x = (mode == kModeDense) ? INFINITY : -FLT_MAX;
     *reinterpret_cast<unsigned*>(&sh.wg_max_x) = ordered_f32(-FLT_MAX);
@@ -698,14 +1026,21 @@ __device__ __forceinline__ int slices_clamped(int s, int64_t vocab) { return s; 
 template <typename Tag, bool kVec>
 __device__ void process_row(Shared& sh, const typename Tag::storage* row, int64_t vocab, const Params& p,
                             const XForm& f, int slices, int slice, uint64_t* pub, uint64_t* pubs, uint32_t* cnt,
-                            RowRec* rec, int32_t* sidx, float* sp, int cand_tok, float cand_x) {
+                            RowRec* rec, int32_t* sidx, float* sp, int cand_tok, float cand_x, uint32_t* list_cnt,
+                            int32_t* list, int32_t list_id, bool raw_ok) {
   const int mode = row_mode(p, vocab);
   init_shared(sh, mode);
   const int k = mode == kModeTopK ? max(p.top_k, 1) : 0;
   const float off_s = mode == kModeFilter ? filter_offset(p) : 0.f;
   const SliceRange r = slice_range(vocab, slices, slice, Tag::kPerVec);
-  ScanOut o = scan_range<Tag, kVec>(sh, row, r.v_begin, r.v_end, f, p.temperature, mode, k, off_s);
-  ScanOut st = finish_slice(sh, o, mode, k, p.temperature, off_s);
+  ScanOut st;
+  if (mode == kModeTopK && raw_ok) {
+    const ScanOut o = scan_topk_raw<Tag, kVec>(sh, row, r.v_begin, r.v_end, f, k);
+    st = finish_topk_raw(sh, o, f, k, p.temperature);
+  } else {
+    const ScanOut o = scan_range<Tag, kVec>(sh, row, r.v_begin, r.v_end, f, p.temperature, mode, k, off_s);
+    st = finish_slice(sh, o, mode, k, p.temperature, off_s);
+  }
   if (slices > 1) {
     if (!merge_slices(sh, st, mode, slices, slice, pub, pubs, cnt, p.temperature)) return;
     if (!sh.overflow) {
@@ -714,7 +1049,7 @@ __device__ void process_row(Shared& sh, const typename Tag::storage* row, int64_
       else if (mode == kModeFilter) compact_ge(sh, ordered_f32(st.mx / p.temperature + off_s));
     }
   }
-  finalize_row<Tag>(sh, st, p, mode, vocab, row, f, rec, sidx, sp, cand_tok, cand_x);
+  finalize_row(sh, st, p, mode, vocab, rec, sidx, sp, cand_tok, cand_x, list_cnt, list, list_id);
 }
 
 template <typename CandT>
@@ -726,7 +1061,7 @@ __device__ __forceinline__ XForm target_xform(const Args& a, int64_t b, int64_t 
   XForm f;
   f.pbits = a.pbits ? a.pbits + b * a.pws : nullptr;
   f.prank = a.pbits ? a.prank + b * a.pws : nullptr;
-  f.padd = a.pbits ? a.padd + b * a.pas : nullptr;
+  f.padd = (a.pbits && a.padd) ? a.padd + b * a.pas : nullptr;
   f.rep = a.prep ? a.prep[b] : 1.f;
   f.quirk = a.quirk;
   f.mbits = a.mask ? a.mask + (a.mask_per_request ? b : row) * a.mrs : nullptr;
@@ -758,7 +1093,8 @@ __global__ __launch_bounds__(kT) void target_scan_kernel(Args a) {
   }
   process_row<TagT, kVec>(sh, rp, a.vocab, p, f, a.s_t, slice, a.pub_t + row * kNBuf,
                           a.pubs_t + row * a.s_t * 2, a.cnt_t + row, a.rec_t + row,
-                          a.sidx_t + row * kCap, a.sp_t + row * kCap, cand_tok, cand_x);
+                          a.sidx_t + row * kCap, a.sp_t + row * kCap, cand_tok, cand_x, a.list_cnt,
+                          a.list_t, static_cast<int32_t>(row), raw_filter_ok(f, a.pnonpos, b));
 }
 
 // First rejected position of request b (width-1 when every drafted token is
@@ -813,7 +1149,96 @@ __global__ __launch_bounds__(kT) void draft_scan_kernel(Args a) {
   const S* rp = static_cast<const S*>(a.draft) + b * a.dsb + static_cast<int64_t>(len) * a.dsk;
   XForm f{nullptr, nullptr, nullptr, 1.f, 0, nullptr};
   process_row<TagD, kVec>(sh, rp, a.vocab, p, f, a.s_d, slice, a.pub_d + b * kNBuf, a.pubs_d + b * a.s_d * 2,
-                          a.cnt_d + b, a.rec_d + b, a.sidx_d + b * kCap, a.sp_d + b * kCap, -1, NAN);
+                          a.cnt_d + b, a.rec_d + b, a.sidx_d + b * kCap, a.sp_d + b * kCap, -1, NAN,
+                          a.list_cnt + 1, a.list_d, static_cast<int32_t>(b), true);
+}
+
+// Exact support of the rows the scan kernels could not resolve from their
+// candidate buffers (listed on a worklist); writes their records.
+__device__ __noinline__ void write_exact_record(Shared& sh, const Exact& ex, int n_f, RowRec* rec, int32_t* sidx,
+                                                float* sp, int cand_tok, float cand_x, float t, int why) {
+  const int tid = threadIdx.x;
+  const bool sparse = ex.n <= kCap && n_f == ex.n;
+  if (sparse)
+    for (int i = tid; i < n_f; i += kT) {
+      const uint64_t kk = sh.buf[i];
+      sidx[i] = key_idx(kk);
+      sp[i] = __expf(key_s(kk) - ex.m) / ex.z;
+    }
+  if (tid == 0) {
+    RowRec r{};
+    r.m = ex.m;
+    r.z = ex.z;
+    r.n = sparse ? n_f : -1;
+    r.flags = sparse ? 0 : kFlagDense;
+    r.why = why | kWhyExact;
+    r.last = sparse ? (n_f > 0 ? sh.buf[n_f - 1] : ~uint64_t(0)) : ex.kcut;
+    if (cand_tok >= 0) {
+      const float sc = cand_x / t;
+      const uint64_t kc = cand_key(sc, cand_tok);
+      r.p_cand = (kc >= r.last && (r.n != 0 || !sparse)) ? __expf(sc - r.m) / r.z : 0.f;
+    }
+    *rec = r;
+  }
+  __syncthreads();
+}
+
+template <typename TagT, typename CandT>
+__global__ __launch_bounds__(kT) void target_fallback_kernel(Args a) {
+  __shared__ Shared sh;
+  const uint32_t n = *a.list_cnt;
+  for (uint32_t li = blockIdx.x; li < n; li += gridDim.x) {
+    const int64_t row = a.list_t[li];
+    const int64_t b = row / a.width;
+    const int j = static_cast<int>(row % a.width);
+    const RowRec prev = a.rec_t[row];
+    Params p{a.temps[b], a.top_ks ? max(a.top_ks[b], 1) : static_cast<int>(a.vocab),
+             a.top_ps ? a.top_ps[b] : 1.f, a.min_ps ? a.min_ps[b] : 0.f};
+    using S = typename TagT::storage;
+    const S* rp = static_cast<const S*>(a.logits) + row * a.lrs;
+    const XForm f = target_xform(a, b, row);
+    int cand_tok = -1;
+    float cand_x = NAN;
+    if (j < a.width - 1) {
+      const int64_t c = cand_at<CandT>(a, b, j);
+      if (c >= 0 && c < a.vocab) {
+        cand_tok = static_cast<int>(c);
+        cand_x = transform1(f, to_f32<S>(rp[c]), c);
+      }
+    }
+    const int mode = row_mode(p, a.vocab);
+    const Exact ex = exact_support<TagT>(sh, rp, a.vocab, f, p, mode, prev.m, prev.z);
+    const int n_f = ex.n <= kCap ? collect<TagT>(sh, rp, a.vocab, f, p.temperature, ex.kcut) : 0;
+    write_exact_record(sh, ex, n_f, a.rec_t + row, a.sidx_t + row * kCap, a.sp_t + row * kCap, cand_tok, cand_x,
+                       p.temperature, prev.why);
+  }
+}
+
+template <typename TagD, typename CandT>
+__global__ __launch_bounds__(kT) void draft_fallback_kernel(Args a) {
+  __shared__ Shared sh;
+  __shared__ int s_len, s_flags;
+  const uint32_t n = *(a.list_cnt + 1);
+  for (uint32_t li = blockIdx.x; li < n; li += gridDim.x) {
+    const int64_t b = a.list_d[li];
+    if (threadIdx.x == 0) s_len = accept_length<CandT>(a, b, &s_flags);
+    __syncthreads();
+    const int len = s_len;
+    const RowRec prev = a.rec_d[b];
+    Params p;
+    p.temperature = a.d_temps ? a.d_temps[b] : a.temps[b];
+    p.top_k = a.d_top_ks ? max(a.d_top_ks[b], 1) : static_cast<int>(a.vocab);
+    p.top_p = a.d_top_ps ? a.d_top_ps[b] : 1.f;
+    p.min_p = a.d_min_ps ? a.d_min_ps[b] : 0.f;
+    using S = typename TagD::storage;
+    const S* rp = static_cast<const S*>(a.draft) + b * a.dsb + static_cast<int64_t>(len) * a.dsk;
+    XForm f{nullptr, nullptr, nullptr, 1.f, 0, nullptr};
+    const int mode = row_mode(p, a.vocab);
+    const Exact ex = exact_support<TagD>(sh, rp, a.vocab, f, p, mode, prev.m, prev.z);
+    const int n_f = ex.n <= kCap ? collect<TagD>(sh, rp, a.vocab, f, p.temperature, ex.kcut) : 0;
+    write_exact_record(sh, ex, n_f, a.rec_d + b, a.sidx_d + b * kCap, a.sp_d + b * kCap, -1, NAN, p.temperature,
+                       prev.why);
+  }
 }
 
 // Probability of token v under the target row record (dense supports only).
@@ -920,6 +1345,10 @@ __global__ __launch_bounds__(kT) void resolve_kernel(Args a) {
   __shared__ float s_mass, s_total;
   const int64_t b = blockIdx.x;
   const int tid = threadIdx.x;
+  if (b == 0 && tid == 0) {
+    atomic_take_u32(a.list_cnt);
+    atomic_take_u32(a.list_cnt + 1);
+  }
   if (tid == 0) s_len = accept_length<CandT>(a, b, &s_flags);
   __syncthreads();
   const int len = s_len;
@@ -1021,7 +1450,7 @@ int pick_slices(int64_t rows, int64_t vocab, int want_wgs, int max_top_k) {
 struct Layout {
   uint64_t counters, scratch;
   uint64_t off_rec_t, off_sidx_t, off_sp_t, off_rec_d, off_sidx_d, off_sp_d, off_pub_t, off_pubs_t, off_pub_d,
-      off_pubs_d;
+      off_pubs_d, off_list_t, off_list_d;
   int s_t, s_d;
 };
 
@@ -1030,7 +1459,7 @@ Layout layout(int64_t batch, int width, int64_t vocab, int max_top_k) {
   const int64_t rows = batch * width;
   l.s_t = pick_slices(rows, vocab, 2048, max_top_k);
   l.s_d = pick_slices(batch, vocab, 1024, max_top_k);
-  l.counters = up256(4 * rows) + up256(4 * batch);
+  l.counters = up256(4 * rows) + up256(4 * batch) + 256;
   uint64_t o = 0;
   l.off_rec_t = o; o += up256(sizeof(RowRec) * rows);
   l.off_sidx_t = o; o += up256(4ull * rows * kCap);
@@ -1042,6 +1471,8 @@ Layout layout(int64_t batch, int width, int64_t vocab, int max_top_k) {
   l.off_pubs_t = o; o += up256(16ull * rows * l.s_t);
   l.off_pub_d = o; o += l.s_d > 1 ? up256(8ull * batch * kNBuf) : 0;
   l.off_pubs_d = o; o += up256(16ull * batch * l.s_d);
+  l.off_list_t = o; o += up256(4ull * rows);
+  l.off_list_d = o; o += up256(4ull * batch);
   l.scratch = o;
   return l;
 }
@@ -1075,7 +1506,7 @@ extern "C" int ls_verify_sample(const ls_verify_sample_args* in, void* counters,
   LS_CHECK(x.draft, LS_ERR_VALUE, "ls_verify_sample: draft rows required");
   LS_CHECK(x.q_mode == 1 || x.draft_token_probs, LS_ERR_VALUE, "ls_verify_sample: q_mode 0 needs draft_token_probs");
   LS_CHECK(x.q_mode == 0 || x.draft_dtype == LS_F32, LS_ERR_DTYPE, "ls_verify_sample: dense q must be fp32");
-  LS_CHECK(!x.pen_bits || (x.pen_rank && x.pen_add), LS_ERR_VALUE, "ls_verify_sample: incomplete penalty tables");
+  LS_CHECK(!x.pen_bits || x.pen_rank, LS_ERR_VALUE, "ls_verify_sample: penalty bitmap without ranks");
   LS_CHECK(!x.pen_bits || x.pen_words_stride >= (x.vocab + 31) / 32, LS_ERR_SHAPE,
            "ls_verify_sample: penalty bitmap stride too small");
   LS_CHECK(!x.vocab_mask || x.mask_row_stride >= (x.vocab + 31) / 32, LS_ERR_SHAPE,
@@ -1093,6 +1524,7 @@ extern "C" int ls_verify_sample(const ls_verify_sample_args* in, void* counters,
   a.temps = x.temperatures; a.top_ks = x.top_ks; a.top_ps = x.top_ps; a.min_ps = x.min_ps;
   a.pbits = x.pen_bits; a.prank = x.pen_rank; a.pws = x.pen_words_stride; a.padd = x.pen_add;
   a.pas = x.pen_add_stride; a.prep = x.pen_repetition; a.quirk = x.pen_verify_quirk;
+  a.pnonpos = x.pen_nonpositive;
   a.mask = reinterpret_cast<const uint32_t*>(x.vocab_mask); a.mrs = x.mask_row_stride;
   a.mask_per_request = x.mask_per_request;
   a.q_mode = x.q_mode; a.dtp = x.draft_token_probs; a.dtp_sb = x.dtp_stride_b;
@@ -1105,6 +1537,7 @@ extern "C" int ls_verify_sample(const ls_verify_sample_args* in, void* counters,
   const int64_t rows = x.batch * x.width;
   a.cnt_t = reinterpret_cast<uint32_t*>(c);
   a.cnt_d = reinterpret_cast<uint32_t*>(c + up256(4 * rows));
+  a.list_cnt = reinterpret_cast<uint32_t*>(c + up256(4 * rows) + up256(4 * x.batch));
   char* s = static_cast<char*>(scratch);
   a.rec_t = reinterpret_cast<RowRec*>(s + l.off_rec_t);
   a.sidx_t = reinterpret_cast<int32_t*>(s + l.off_sidx_t);
@@ -1116,12 +1549,21 @@ extern "C" int ls_verify_sample(const ls_verify_sample_args* in, void* counters,
   a.pubs_t = reinterpret_cast<uint64_t*>(s + l.off_pubs_t);
   a.pub_d = reinterpret_cast<uint64_t*>(s + l.off_pub_d);
   a.pubs_d = reinterpret_cast<uint64_t*>(s + l.off_pubs_d);
+  a.list_t = reinterpret_cast<int32_t*>(s + l.off_list_t);
+  a.list_d = reinterpret_cast<int32_t*>(s + l.off_list_d);
   a.s_t = l.s_t;
   a.s_d = l.s_d;
   hipStream_t st = static_cast<hipStream_t>(stream);
 
   const dim3 g_t(static_cast<unsigned>(rows * l.s_t)), g_d(static_cast<unsigned>(x.batch * l.s_d)),
-      g_r(static_cast<unsigned>(x.batch));
+      g_r(static_cast<unsigned>(x.batch)), g_f(static_cast<unsigned>(rows < 256 ? rows : 256)),
+      g_fd(static_cast<unsigned>(x.batch < 256 ? x.batch : 256));
+  void* const* ev = x.timing_events;
+#define LS_EVENT(i)                                                                              \
+  do {                                                                                           \
+    if (hipEventRecord(static_cast<hipEvent_t>(ev[i]), st) != hipSuccess)                        \
+      return fail(LS_ERR_LAUNCH, "ls_verify_sample: hipEventRecord failed");                     \
+  } while (0)
   const bool tvec_ok = aligned16(x.logits);
   const bool dvec_ok = aligned16(x.draft);
 #define LS_RUN(TT, TD, CT)                                                                                    \
@@ -1130,16 +1572,24 @@ extern "C" int ls_verify_sample(const ls_verify_sample_args* in, void* counters,
     using DS = typename TD::storage;                                                                          \
     const bool tv = tvec_ok && (x.logits_row_stride * sizeof(TS)) % 16 == 0;                                  \
     const bool dv = dvec_ok && (x.draft_stride_b * sizeof(DS)) % 16 == 0 && (x.draft_stride_k * sizeof(DS)) % 16 == 0; \
+    if (ev) LS_EVENT(0);                                                                                      \
     if (tv) target_scan_kernel<TT, true, CT><<<g_t, rs::kT, 0, st>>>(a);                                     \
     else target_scan_kernel<TT, false, CT><<<g_t, rs::kT, 0, st>>>(a);                                       \
+    LS_LAUNCH_CHECK();                                                                                        \
+    if (ev) LS_EVENT(1);                                                                                      \
+    target_fallback_kernel<TT, CT><<<g_f, rs::kT, 0, st>>>(a);                                                \
     LS_LAUNCH_CHECK();                                                                                        \
     if (x.q_mode == 0) {                                                                                      \
       if (dv) draft_scan_kernel<TD, true, CT><<<g_d, rs::kT, 0, st>>>(a);                                    \
       else draft_scan_kernel<TD, false, CT><<<g_d, rs::kT, 0, st>>>(a);                                      \
       LS_LAUNCH_CHECK();                                                                                      \
+      draft_fallback_kernel<TD, CT><<<g_fd, rs::kT, 0, st>>>(a);                                              \
+      LS_LAUNCH_CHECK();                                                                                      \
     }                                                                                                         \
+    if (ev) LS_EVENT(2);                                                                                      \
     resolve_kernel<TT, TD, CT><<<g_r, rs::kT, 0, st>>>(a);                                                    \
     LS_LAUNCH_CHECK();                                                                                        \
+    if (ev) LS_EVENT(3);                                                                                      \
     return LS_OK;                                                                                             \
   } while (0)
 #define LS_CAND(TT, TD)                                             \
@@ -1156,5 +1606,6 @@ extern "C" int ls_verify_sample(const ls_verify_sample_args* in, void* counters,
 #undef LS_DRAFT
 #undef LS_CAND
 #undef LS_RUN
+#undef LS_EVENT
   return fail(LS_ERR_DTYPE, "ls_verify_sample: logits must be bf16, fp16 or fp32");
 }

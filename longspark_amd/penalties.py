@@ -23,8 +23,10 @@ class PenaltyTables:
     rank: torch.Tensor          # [B, ceil(V/32)] int32
     add: torch.Tensor           # [B, H] float32
     distinct: torch.Tensor      # [B] int32
+    nonpositive: torch.Tensor   # [B] int32: 1 where every additive value is <= 0
     repetition: Optional[torch.Tensor]  # [B] float32 or None
     verify_quirk: bool = False
+    has_additive: bool = True   # False: frequency and presence are off (add is all zero)
 
 
 def build_penalty_tables(history: torch.Tensor, vocab: int, *, frequency=None, presence=None, repetition=None,
@@ -48,6 +50,7 @@ def build_penalty_tables(history: torch.Tensor, vocab: int, *, frequency=None, p
     rank = torch.empty(batch, words, dtype=torch.int32, device=dev)
     add = torch.empty(batch, max(cap, 1), dtype=torch.float32, device=dev)
     distinct = torch.empty(batch, dtype=torch.int32, device=dev)
+    nonpositive = torch.empty(batch, dtype=torch.int32, device=dev)
 
     def vec(t, name):
         if t is None:
@@ -64,9 +67,10 @@ def build_penalty_tables(history: torch.Tensor, vocab: int, *, frequency=None, p
         history_lens = history_lens.to(torch.int32).contiguous()
     _lib.call("ls_penalty_tables", history.data_ptr(), history.stride(0), _lib.ptr(history_lens), batch, cap, vocab,
               _lib.ptr(frequency), _lib.ptr(presence), bits.data_ptr(), rank.data_ptr(), words, add.data_ptr(),
-              add.shape[1], distinct.data_ptr(), _lib.stream_of(dev))
-    return PenaltyTables(bits=bits, rank=rank, add=add, distinct=distinct, repetition=repetition,
-                         verify_quirk=verify_quirk)
+              add.shape[1], distinct.data_ptr(), nonpositive.data_ptr(), _lib.stream_of(dev))
+    return PenaltyTables(bits=bits, rank=rank, add=add, distinct=distinct, nonpositive=nonpositive,
+                         repetition=repetition,
+                         verify_quirk=verify_quirk, has_additive=frequency is not None or presence is not None)
 
 
 def adjust_logits_(logits: torch.Tensor, *, rows_per_request: int, tables: Optional[PenaltyTables] = None,
@@ -92,7 +96,7 @@ def adjust_logits_(logits: torch.Tensor, *, rows_per_request: int, tables: Optio
     _lib.call("ls_adjust_logits", logits.data_ptr(), _lib.dtype_code(logits), logits.stride(0), rows, vocab,
               rows_per_request,
               _lib.ptr(t.bits) if t else None, _lib.ptr(t.rank) if t else None, t.bits.stride(0) if t else 0,
-              _lib.ptr(t.add) if t else None, t.add.stride(0) if t else 0,
+              _lib.ptr(t.add) if (t and t.has_additive) else None, t.add.stride(0) if t else 0,
               _lib.ptr(t.repetition) if t else None, int(bool(t and t.verify_quirk)),
               _lib.ptr(vocab_mask), vocab_mask.stride(0) if vocab_mask is not None else 0,
               rows_per_request if mask_per_request else 1,

@@ -141,7 +141,8 @@ def verify_sample(*, logits: torch.Tensor, candidates: torch.Tensor, width: int,
                   draft_logits: Optional[torch.Tensor] = None, draft_probs: Optional[torch.Tensor] = None,
                   draft_temperatures=None, draft_top_ks=None, draft_top_ps=None, draft_min_ps=None,
                   penalties=None, vocab_mask: Optional[torch.Tensor] = None, mask_per_request: bool = False,
-                  cand_first_col: int = 1, return_p_cand: bool = False, check: bool = False):
+                  cand_first_col: int = 1, return_p_cand: bool = False, check: bool = False,
+                  timing_events=None):
     """Fused stochastic verify of a drafted block (one call, three kernels).
 
     Target: ``logits`` ``[B*width, V]`` (bf16/fp16/fp32) with penalties
@@ -155,8 +156,9 @@ def verify_sample(*, logits: torch.Tensor, candidates: torch.Tensor, width: int,
     Randomness: ``uniforms [B, width-1]`` and ``final_uniforms [B]`` fp32.
     Returns ``(accept_lens i32[B], bonus i64[B])`` (plus the per-drafted-token
     target probabilities ``[B, width-1]`` with ``return_p_cand``).  With
-    ``check`` the call synchronises and raises if a request exceeded the
-    kernel's support capacity (such requests get -1 in both outputs).
+    ``check`` the call synchronises and raises if a request could not be
+    resolved (such requests get -1 in both outputs).  ``timing_events``: an
+    optional ctypes array of 4 hipEvent_t recorded around the three kernels.
     """
     what = "verify_sample"
     logits = _rows_view(logits, width, what)
@@ -220,8 +222,9 @@ def verify_sample(*, logits: torch.Tensor, candidates: torch.Tensor, width: int,
     t = penalties
     if t is not None:
         a.pen_bits, a.pen_rank, a.pen_words_stride = t.bits.data_ptr(), t.rank.data_ptr(), t.bits.stride(0)
-        a.pen_add, a.pen_add_stride = t.add.data_ptr(), t.add.stride(0)
+        a.pen_add, a.pen_add_stride = (t.add.data_ptr() if t.has_additive else None), t.add.stride(0)
         a.pen_repetition, a.pen_verify_quirk = _lib.ptr(t.repetition), int(bool(t.verify_quirk))
+        a.pen_nonpositive = t.nonpositive.data_ptr()
     if vocab_mask is not None:
         a.vocab_mask, a.mask_row_stride, a.mask_per_request = vocab_mask.data_ptr(), vocab_mask.stride(0), \
             int(mask_per_request)
@@ -236,6 +239,8 @@ def verify_sample(*, logits: torch.Tensor, candidates: torch.Tensor, width: int,
         final_uniforms.data_ptr()
     a.accept_lens, a.bonus, a.p_cand_out, a.status = accept.data_ptr(), bonus.data_ptr(), _lib.ptr(p_cand), \
         status.data_ptr()
+    if timing_events is not None:
+        a.timing_events = _lib.ctypes.cast(timing_events, _lib.ctypes.c_void_p)
     cnt, scr = _lib.workspaces.get(*_lib.workspace_sizes("ls_verify_sample_workspace", batch, width, vocab, mk), dev)
     _lib.call("ls_verify_sample", ctypes_byref(a), cnt.data_ptr(), cnt.numel(), scr.data_ptr(), scr.numel(),
               _lib.stream_of(dev))

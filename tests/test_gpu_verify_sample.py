@@ -81,6 +81,20 @@ def test_topk_repetition_history(dev):
     check_case(dev, d, label="k50 p0.95 rep1.05")
 
 
+def test_topk_negative_presence_exact_loop(dev):
+    # A negative presence penalty raises repeated tokens: the raw-logit filter
+    # is not valid, so these rows take the exact per-element loop.
+    d = workloads.stochastic_inputs(6, 16, seed=18, temperature=0.9, top_k=64, top_p=0.9, history_len=3000,
+                                    repetition=1.1, presence=-0.7, frequency=0.05)
+    check_case(dev, d, label="k64 negative presence")
+
+
+def test_topk_large_k_full_vocab(dev):
+    d = workloads.stochastic_inputs(4, 8, seed=19, temperature=1.1, top_k=700, top_p=0.97, history_len=500,
+                                    repetition=1.3)
+    check_case(dev, d, label="k700")
+
+
 def test_verify_quirk(dev):
     d = workloads.stochastic_inputs(4, 16, seed=14, temperature=0.8, top_k=40, top_p=0.9, history_len=1024,
                                     repetition=1.2, presence=0.4, frequency=0.3, mask_density=0.5)
