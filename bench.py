@@ -169,7 +169,8 @@ class StochasticVerify:
             logits=d["logits"], candidates=d["candidates"], width=self.width, temperatures=p.temperatures,
             top_ks=p.top_ks, top_ps=p.top_ps, min_ps=p.min_ps, max_top_k=50, draft_logits=d["draft_logits"],
             draft_token_probs=d["draft_token_probs"], draft_top_ks=p.top_ks, draft_top_ps=p.top_ps,
-            uniforms=d["uniforms"], final_uniforms=d["final_uniforms"], penalties=tables, timing_events=ev)
+            uniforms=d["uniforms"], final_uniforms=d["final_uniforms"], penalties=tables, timing_events=ev,
+            scan_hint=1)
 
     def kernel_times_ms(self):
         n = self.step_idx

@@ -242,6 +242,11 @@ typedef struct {
    * before the target scan, after it, before the resolve kernel and after it
    * (the middle interval holds the fallback and draft-scan kernels). */
   void* const* timing_events;
+  /* Which row-scan kernels to launch: 0 = both (each row runs in the one for
+   * its path), 1 = only the raw-logit top-k scan (for callers that know every
+   * row is top-k with repetition >= 1 and additive penalties <= 0; other rows
+   * are still resolved exactly, more slowly), 2 = only the exact scan. */
+  int32_t scan_hint;
 } ls_verify_sample_args;
 
 LS_API int ls_verify_sample_workspace(int64_t batch, int32_t width, int64_t vocab, int32_t max_top_k,

@@ -53,7 +53,7 @@ class VerifySampleArgs(ctypes.Structure):
         ("draft_temperatures", P), ("draft_top_ks", P), ("draft_top_ps", P), ("draft_min_ps", P),
         ("uniforms", P), ("uniform_stride_b", I64), ("final_uniforms", P),
         ("accept_lens", P), ("bonus", P), ("p_cand_out", P), ("status", P),
-        ("timing_events", P),
+        ("timing_events", P), ("scan_hint", I32),
     ]
 
 

@@ -36,6 +36,7 @@ enum RowFlags : int {
   kFlagOverflow = 1,  // support could not be determined from the candidate buffer
   kFlagDense = 2,     // support is the whole vocabulary
   kFlagSkip = 4,      // row not processed (draft row of an all-accepted request)
+  kFlagUnscanned = 8, // row statistics not computed (fallback computes them)
 };
 
 // Per-request sampling parameters of one row.
@@ -170,7 +171,7 @@ __device__ __forceinline__ void append_vec(Shared& sh, const float* x, float tau
 // Ordered-s (high 32 bits of a key) of the k-th largest entry among buf[0..n)
 // (ties counted), by a 4 x 8-bit MSB-first radix select.  k in [1, n].
 // Must be called by all threads of the workgroup.
-__device__ __noinline__ uint32_t select_kth_s(Shared& sh, int n, int k) {
+__device__ __forceinline__ uint32_t select_kth_s(Shared& sh, int n, int k) {
   uint32_t prefix = 0, pmask = 0;
   int remaining = k;
   const int tid = threadIdx.x;
@@ -220,7 +221,7 @@ __device__ __noinline__ uint32_t select_kth_s(Shared& sh, int n, int k) {
 }
 
 // Keep only entries whose ordered-s is >= thr (stable).  All threads.
-__device__ __noinline__ void compact_ge(Shared& sh, uint32_t thr) {
+__device__ __forceinline__ void compact_ge(Shared& sh, uint32_t thr) {
   const int n = min(sh.count, kNBuf);
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
@@ -255,7 +256,7 @@ __device__ __noinline__ void compact_ge(Shared& sh, uint32_t thr) {
 }
 
 // Sort buf[0..n) descending (bitonic, padded with zeros to a power of two).
-__device__ __noinline__ void sort_desc(Shared& sh, int n) {
+__device__ __forceinline__ void sort_desc(Shared& sh, int n) {
   int np = 1;
   while (np < n) np <<= 1;
   const int tid = threadIdx.x;

@@ -93,6 +93,7 @@ struct Args {
   uint64_t* pubs_t;   // [B*K, S_t, 2]
   uint64_t* pub_d;    // [B, kNBuf]
   uint64_t* pubs_d;   // [B, S_d, 2]
+  int hint;            // which scan kernels the launcher runs (Hint)
   uint32_t* list_cnt;  // counters [2]: rows waiting for the exact fallback (target, draft)
   int32_t* list_t;     // [B*K]
   int32_t* list_d;     // [B]
@@ -123,11 +124,12 @@ enum Why : int {
   kWhySort = 16,      // more than 2048 candidates at finalisation
   kWhyNucleus = 32,   // top-p nucleus extends past the candidates
   kWhyCap = 64,       // support larger than a record holds
+  kWhyHint = 128,     // raw-only launch: row needs the exact path, never scanned
   kWhyExact = 256,    // record written by the fallback
 };
 
 // k-th largest (ties counted) of the kT values v (one per thread), k <= kT.
-__device__ __noinline__ float kth_largest_of_block(Shared& sh, float v, int k) {
+__device__ __forceinline__ float kth_largest_of_block(Shared& sh, float v, int k) {
   float* vals = reinterpret_cast<float*>(sh.hist);  // kT floats
   __shared__ float res;
   const int tid = threadIdx.x;
@@ -148,7 +150,7 @@ __device__ __noinline__ float kth_largest_of_block(Shared& sh, float v, int k) {
 }
 
 // Compaction of an over-full candidate buffer (all threads; rare).
-__device__ __noinline__ void compact_slow(Shared& sh, int mode, int k, float t, float off_s) {
+__device__ __forceinline__ void compact_slow(Shared& sh, int mode, int k, float t, float off_s) {
   const int count = sh.count;
   if (count > kNBuf) {
     __syncthreads();
@@ -391,7 +393,7 @@ __device__ __forceinline__ void append_raw(Shared& sh, const float* x, float tau
 }
 
 // Transform the buffered entries appended since the last transform (all threads).
-__device__ __noinline__ void transform_pending(Shared& sh, const XForm& f) {
+__device__ __forceinline__ void transform_pending(Shared& sh, const XForm& f) {
   const int n = min(sh.count, kNBuf);
   if (f.pbits || f.mbits) {
     for (int i = sh.ntrans + static_cast<int>(threadIdx.x); i < n; i += kT) {
@@ -408,7 +410,7 @@ __device__ __noinline__ void transform_pending(Shared& sh, const XForm& f) {
 // Transform, select the k-th largest transformed value and keep the entries
 // within the rounding margin of it (all threads).  Returns the new raw
 // threshold.
-__device__ __noinline__ float compact_raw(Shared& sh, const XForm& f, int k) {
+__device__ __forceinline__ float compact_raw(Shared& sh, const XForm& f, int k) {
   transform_pending(sh, f);
   const int n = min(sh.count, kNBuf);
   if (n <= k) return -FLT_MAX;
@@ -528,7 +530,7 @@ __device__ ScanOut scan_topk_raw(Shared& sh, const typename Tag::storage* row, i
 
 // End of a raw-filter slice: transform what is pending, keep the top k within
 // the rounding margin, and re-key the survivors by scaled logit x / T.
-__device__ __noinline__ ScanOut finish_topk_raw(Shared& sh, const ScanOut& o, const XForm& f, int k, float t) {
+__device__ __forceinline__ ScanOut finish_topk_raw(Shared& sh, const ScanOut& o, const XForm& f, int k, float t) {
   ScanOut r;
   r.mx = block_max(sh, o.mx);  // raw maximum: an upper bound of the transformed one
   r.mz = r.mx;
@@ -555,7 +557,7 @@ __device__ __forceinline__ bool raw_filter_ok(const XForm& f, const int32_t* non
 
 // After the scan of a slice: final compaction of the slice's candidates and
 // workgroup-wide statistics.  Returns (max x, reference max, z).
-__device__ __noinline__ ScanOut finish_slice(Shared& sh, const ScanOut& o, int mode, int k, float t, float off_s) {
+__device__ __forceinline__ ScanOut finish_slice(Shared& sh, const ScanOut& o, int mode, int k, float t, float off_s) {
   ScanOut r;
   r.mx = block_max(sh, o.mx);
   if (mode != kModeTopK) {
@@ -585,7 +587,7 @@ __device__ __noinline__ ScanOut finish_slice(Shared& sh, const ScanOut& o, int m
 // Index of the first entry i < n (entries sorted by key, e_i = exp(s_i - m))
 // at which the running sum before i, divided by `denom`, exceeds `limit`;
 // n if none.  Also returns the full sum of e_i / denom through *total.
-__device__ __noinline__ int first_excl_exceeds(Shared& sh, int n, float m, float denom, float limit, float* total) {
+__device__ __forceinline__ int first_excl_exceeds(Shared& sh, int n, float m, float denom, float limit, float* total) {
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1), wid = tid / kWave;
   __shared__ int found;
@@ -770,6 +772,22 @@ __device__ __noinline__ int collect(Shared& sh, const typename Tag::storage* row
   return n;
 }
 
+// Maximum transformed logit and the dense normaliser sum exp((x - max) / T)
+// of a row that was never scanned (two passes; fallback only).
+template <typename Tag>
+__device__ __noinline__ void row_stats(Shared& sh, const typename Tag::storage* row, int64_t vocab, const XForm& f,
+                                       float t, float* m_x, float* z) {
+  float mx = -FLT_MAX;
+  for (int64_t v = threadIdx.x; v < vocab; v += kT)
+    mx = fmaxf(mx, transform1(f, to_f32<typename Tag::storage>(row[v]), v));
+  mx = block_max(sh, mx);
+  float acc = 0.f;
+  for (int64_t v = threadIdx.x; v < vocab; v += kT)
+    acc += __expf((transform1(f, to_f32<typename Tag::storage>(row[v]), v) - mx) / t);
+  *m_x = mx;
+  *z = block_sum(sh, acc);
+}
+
 struct Exact {
   float m, z;
   uint64_t kcut;  // support = keys >= kcut
@@ -820,7 +838,7 @@ __device__ __noinline__ Exact exact_support(Shared& sh, const typename Tag::stor
 // hold the support, from the row itself) and write the row record.  `cand_x`
 // is the transformed logit of the drafted token this row verifies.  All
 // threads.
-__device__ __noinline__ void finalize_row(Shared& sh, const ScanOut& st, const Params& p, int mode, int64_t vocab,
+__device__ __forceinline__ void finalize_row(Shared& sh, const ScanOut& st, const Params& p, int mode, int64_t vocab,
                                           RowRec* rec, int32_t* sidx, float* sp, int cand_tok, float cand_x,
                                           uint32_t* list_cnt, int32_t* list, int32_t list_id) {
   const int tid = threadIdx.x;
@@ -944,7 +962,7 @@ __device__ __noinline__ void finalize_row(Shared& sh, const ScanOut& st, const P
 // Publish this slice's candidates and statistics, arrive on the row counter,
 // and, in the last slice to arrive, gather all slices into LDS.  Returns true
 // in the workgroup that continues with the row.
-__device__ __noinline__ bool merge_slices(Shared& sh, ScanOut& st, int mode, int slices, int slice, uint64_t* pub,
+__device__ __forceinline__ bool merge_slices(Shared& sh, ScanOut& st, int mode, int slices, int slice, uint64_t* pub,
                              uint64_t* pubs, uint32_t* counter, float t) {
   const int tid = threadIdx.x;
   __shared__ int is_last;
@@ -1023,18 +1041,40 @@ __device__ __forceinline__ float filter_offset(const Params& p) {
 
 __device__ __forceinline__ int slices_clamped(int s, int64_t vocab) { return s; }
 
-template <typename Tag, bool kVec>
+// kPath: kPathRaw scans only rows eligible for the raw-logit top-k filter,
+// kPathExact only the others (or every row when the launcher runs the exact
+// kernel alone).  With the raw kernel alone (hint), an ineligible row is
+// handed to the exact fallback unscanned.
+enum Path : int { kPathRaw = 0, kPathExact = 1 };
+enum Hint : int { kHintBoth = 0, kHintRawOnly = 1, kHintExactOnly = 2 };
+
+template <typename Tag, bool kVec, int kPath>
 __device__ void process_row(Shared& sh, const typename Tag::storage* row, int64_t vocab, const Params& p,
                             const XForm& f, int slices, int slice, uint64_t* pub, uint64_t* pubs, uint32_t* cnt,
                             RowRec* rec, int32_t* sidx, float* sp, int cand_tok, float cand_x, uint32_t* list_cnt,
-                            int32_t* list, int32_t list_id, bool raw_ok) {
+                            int32_t* list, int32_t list_id, bool raw_ok, int hint) {
   const int mode = row_mode(p, vocab);
+  const bool raw = mode == kModeTopK && raw_ok;
+  if constexpr (kPath == kPathRaw) {
+    if (!raw) {
+      if (hint == kHintRawOnly && slice == 0 && threadIdx.x == 0) {
+        RowRec rr{};
+        rr.flags = kFlagOverflow | kFlagUnscanned;
+        rr.why = kWhyHint;
+        *rec = rr;
+        list[atomic_add_u32(list_cnt, 1u)] = list_id;
+      }
+      return;
+    }
+  } else {
+    if (raw && hint != kHintExactOnly) return;
+  }
   init_shared(sh, mode);
   const int k = mode == kModeTopK ? max(p.top_k, 1) : 0;
   const float off_s = mode == kModeFilter ? filter_offset(p) : 0.f;
   const SliceRange r = slice_range(vocab, slices, slice, Tag::kPerVec);
   ScanOut st;
-  if (mode == kModeTopK && raw_ok) {
+  if constexpr (kPath == kPathRaw) {
     const ScanOut o = scan_topk_raw<Tag, kVec>(sh, row, r.v_begin, r.v_end, f, k);
     st = finish_topk_raw(sh, o, f, k, p.temperature);
   } else {
@@ -1070,7 +1110,7 @@ __device__ __forceinline__ XForm target_xform(const Args& a, int64_t b, int64_t 
 
 // --------------------------------------------------------------- kernels ---
 
-template <typename TagT, bool kVec, typename CandT>
+template <typename TagT, bool kVec, typename CandT, int kPath>
 __global__ __launch_bounds__(kT) void target_scan_kernel(Args a) {
   __shared__ Shared sh;
   const int64_t row = blockIdx.x / a.s_t;
@@ -1091,10 +1131,10 @@ __global__ __launch_bounds__(kT) void target_scan_kernel(Args a) {
       cand_x = transform1(f, to_f32<S>(rp[c]), c);
     }
   }
-  process_row<TagT, kVec>(sh, rp, a.vocab, p, f, a.s_t, slice, a.pub_t + row * kNBuf,
-                          a.pubs_t + row * a.s_t * 2, a.cnt_t + row, a.rec_t + row,
-                          a.sidx_t + row * kCap, a.sp_t + row * kCap, cand_tok, cand_x, a.list_cnt,
-                          a.list_t, static_cast<int32_t>(row), raw_filter_ok(f, a.pnonpos, b));
+  process_row<TagT, kVec, kPath>(sh, rp, a.vocab, p, f, a.s_t, slice, a.pub_t + row * kNBuf,
+                                 a.pubs_t + row * a.s_t * 2, a.cnt_t + row, a.rec_t + row,
+                                 a.sidx_t + row * kCap, a.sp_t + row * kCap, cand_tok, cand_x, a.list_cnt,
+                                 a.list_t, static_cast<int32_t>(row), raw_filter_ok(f, a.pnonpos, b), a.hint);
 }
 
 // First rejected position of request b (width-1 when every drafted token is
@@ -1123,7 +1163,7 @@ __device__ int accept_length(const Args& a, int64_t b, int* flags) {
   return len;
 }
 
-template <typename TagD, bool kVec, typename CandT>
+template <typename TagD, bool kVec, typename CandT, int kPath>
 __global__ __launch_bounds__(kT) void draft_scan_kernel(Args a) {
   __shared__ Shared sh;
   __shared__ int s_len, s_flags;
@@ -1133,7 +1173,8 @@ __global__ __launch_bounds__(kT) void draft_scan_kernel(Args a) {
   __syncthreads();
   const int len = s_len;
   if (len >= a.width - 1 || s_flags) {
-    if (slice == 0 && threadIdx.x == 0) {
+    const bool writer = (kPath == kPathExact) == (a.hint != kHintRawOnly);
+    if (writer && slice == 0 && threadIdx.x == 0) {
       RowRec r{};
       r.flags = kFlagSkip;
       a.rec_d[b] = r;
@@ -1148,9 +1189,10 @@ __global__ __launch_bounds__(kT) void draft_scan_kernel(Args a) {
   using S = typename TagD::storage;
   const S* rp = static_cast<const S*>(a.draft) + b * a.dsb + static_cast<int64_t>(len) * a.dsk;
   XForm f{nullptr, nullptr, nullptr, 1.f, 0, nullptr};
-  process_row<TagD, kVec>(sh, rp, a.vocab, p, f, a.s_d, slice, a.pub_d + b * kNBuf, a.pubs_d + b * a.s_d * 2,
-                          a.cnt_d + b, a.rec_d + b, a.sidx_d + b * kCap, a.sp_d + b * kCap, -1, NAN,
-                          a.list_cnt + 1, a.list_d, static_cast<int32_t>(b), true);
+  process_row<TagD, kVec, kPath>(sh, rp, a.vocab, p, f, a.s_d, slice, a.pub_d + b * kNBuf,
+                                 a.pubs_d + b * a.s_d * 2, a.cnt_d + b, a.rec_d + b, a.sidx_d + b * kCap,
+                                 a.sp_d + b * kCap, -1, NAN, a.list_cnt + 1, a.list_d, static_cast<int32_t>(b), true,
+                                 a.hint);
 }
 
 // Exact support of the rows the scan kernels could not resolve from their
@@ -1207,7 +1249,9 @@ __global__ __launch_bounds__(kT) void target_fallback_kernel(Args a) {
       }
     }
     const int mode = row_mode(p, a.vocab);
-    const Exact ex = exact_support<TagT>(sh, rp, a.vocab, f, p, mode, prev.m, prev.z);
+    float m_x = prev.m, z = prev.z;
+    if (prev.flags & kFlagUnscanned) row_stats<TagT>(sh, rp, a.vocab, f, p.temperature, &m_x, &z);
+    const Exact ex = exact_support<TagT>(sh, rp, a.vocab, f, p, mode, m_x, z);
     const int n_f = ex.n <= kCap ? collect<TagT>(sh, rp, a.vocab, f, p.temperature, ex.kcut) : 0;
     write_exact_record(sh, ex, n_f, a.rec_t + row, a.sidx_t + row * kCap, a.sp_t + row * kCap, cand_tok, cand_x,
                        p.temperature, prev.why);
@@ -1234,7 +1278,9 @@ __global__ __launch_bounds__(kT) void draft_fallback_kernel(Args a) {
     const S* rp = static_cast<const S*>(a.draft) + b * a.dsb + static_cast<int64_t>(len) * a.dsk;
     XForm f{nullptr, nullptr, nullptr, 1.f, 0, nullptr};
     const int mode = row_mode(p, a.vocab);
-    const Exact ex = exact_support<TagD>(sh, rp, a.vocab, f, p, mode, prev.m, prev.z);
+    float m_x = prev.m, z = prev.z;
+    if (prev.flags & kFlagUnscanned) row_stats<TagD>(sh, rp, a.vocab, f, p.temperature, &m_x, &z);
+    const Exact ex = exact_support<TagD>(sh, rp, a.vocab, f, p, mode, m_x, z);
     const int n_f = ex.n <= kCap ? collect<TagD>(sh, rp, a.vocab, f, p.temperature, ex.kcut) : 0;
     write_exact_record(sh, ex, n_f, a.rec_d + b, a.sidx_d + b * kCap, a.sp_d + b * kCap, -1, NAN, p.temperature,
                        prev.why);
@@ -1503,6 +1549,7 @@ extern "C" int ls_verify_sample(const ls_verify_sample_args* in, void* counters,
   LS_CHECK(x.logits && x.candidates && x.temperatures && x.uniforms && x.final_uniforms && x.accept_lens && x.bonus,
            LS_ERR_VALUE, "ls_verify_sample: null required pointer");
   LS_CHECK(x.q_mode == 0 || x.q_mode == 1, LS_ERR_VALUE, "ls_verify_sample: q_mode must be 0 or 1");
+  LS_CHECK(x.scan_hint >= 0 && x.scan_hint <= 2, LS_ERR_VALUE, "ls_verify_sample: scan_hint must be 0, 1 or 2");
   LS_CHECK(x.draft, LS_ERR_VALUE, "ls_verify_sample: draft rows required");
   LS_CHECK(x.q_mode == 1 || x.draft_token_probs, LS_ERR_VALUE, "ls_verify_sample: q_mode 0 needs draft_token_probs");
   LS_CHECK(x.q_mode == 0 || x.draft_dtype == LS_F32, LS_ERR_DTYPE, "ls_verify_sample: dense q must be fp32");
@@ -1553,6 +1600,7 @@ extern "C" int ls_verify_sample(const ls_verify_sample_args* in, void* counters,
   a.list_d = reinterpret_cast<int32_t*>(s + l.off_list_d);
   a.s_t = l.s_t;
   a.s_d = l.s_d;
+  a.hint = x.scan_hint;
   hipStream_t st = static_cast<hipStream_t>(stream);
 
   const dim3 g_t(static_cast<unsigned>(rows * l.s_t)), g_d(static_cast<unsigned>(x.batch * l.s_d)),
@@ -1573,16 +1621,30 @@ extern "C" int ls_verify_sample(const ls_verify_sample_args* in, void* counters,
     const bool tv = tvec_ok && (x.logits_row_stride * sizeof(TS)) % 16 == 0;                                  \
     const bool dv = dvec_ok && (x.draft_stride_b * sizeof(DS)) % 16 == 0 && (x.draft_stride_k * sizeof(DS)) % 16 == 0; \
     if (ev) LS_EVENT(0);                                                                                      \
-    if (tv) target_scan_kernel<TT, true, CT><<<g_t, rs::kT, 0, st>>>(a);                                     \
-    else target_scan_kernel<TT, false, CT><<<g_t, rs::kT, 0, st>>>(a);                                       \
-    LS_LAUNCH_CHECK();                                                                                        \
+    if (a.hint != kHintExactOnly) {                                                                           \
+      if (tv) target_scan_kernel<TT, true, CT, kPathRaw><<<g_t, rs::kT, 0, st>>>(a);                         \
+      else target_scan_kernel<TT, false, CT, kPathRaw><<<g_t, rs::kT, 0, st>>>(a);                           \
+      LS_LAUNCH_CHECK();                                                                                      \
+    }                                                                                                         \
+    if (a.hint != kHintRawOnly) {                                                                             \
+      if (tv) target_scan_kernel<TT, true, CT, kPathExact><<<g_t, rs::kT, 0, st>>>(a);                       \
+      else target_scan_kernel<TT, false, CT, kPathExact><<<g_t, rs::kT, 0, st>>>(a);                         \
+      LS_LAUNCH_CHECK();                                                                                      \
+    }                                                                                                         \
     if (ev) LS_EVENT(1);                                                                                      \
     target_fallback_kernel<TT, CT><<<g_f, rs::kT, 0, st>>>(a);                                                \
     LS_LAUNCH_CHECK();                                                                                        \
     if (x.q_mode == 0) {                                                                                      \
-      if (dv) draft_scan_kernel<TD, true, CT><<<g_d, rs::kT, 0, st>>>(a);                                    \
-      else draft_scan_kernel<TD, false, CT><<<g_d, rs::kT, 0, st>>>(a);                                      \
-      LS_LAUNCH_CHECK();                                                                                      \
+      if (a.hint != kHintExactOnly) {                                                                         \
+        if (dv) draft_scan_kernel<TD, true, CT, kPathRaw><<<g_d, rs::kT, 0, st>>>(a);                        \
+        else draft_scan_kernel<TD, false, CT, kPathRaw><<<g_d, rs::kT, 0, st>>>(a);                          \
+        LS_LAUNCH_CHECK();                                                                                    \
+      }                                                                                                       \
+      if (a.hint != kHintRawOnly) {                                                                           \
+        if (dv) draft_scan_kernel<TD, true, CT, kPathExact><<<g_d, rs::kT, 0, st>>>(a);                      \
+        else draft_scan_kernel<TD, false, CT, kPathExact><<<g_d, rs::kT, 0, st>>>(a);                        \
+        LS_LAUNCH_CHECK();                                                                                    \
+      }                                                                                                       \
       draft_fallback_kernel<TD, CT><<<g_fd, rs::kT, 0, st>>>(a);                                              \
       LS_LAUNCH_CHECK();                                                                                      \
     }                                                                                                         \

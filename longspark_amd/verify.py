@@ -142,7 +142,7 @@ def verify_sample(*, logits: torch.Tensor, candidates: torch.Tensor, width: int,
                   draft_temperatures=None, draft_top_ks=None, draft_top_ps=None, draft_min_ps=None,
                   penalties=None, vocab_mask: Optional[torch.Tensor] = None, mask_per_request: bool = False,
                   cand_first_col: int = 1, return_p_cand: bool = False, check: bool = False,
-                  timing_events=None):
+                  timing_events=None, scan_hint: int = 0):
     """Fused stochastic verify of a drafted block (one call, three kernels).
 
     Target: ``logits`` ``[B*width, V]`` (bf16/fp16/fp32) with penalties
@@ -158,7 +158,11 @@ def verify_sample(*, logits: torch.Tensor, candidates: torch.Tensor, width: int,
     target probabilities ``[B, width-1]`` with ``return_p_cand``).  With
     ``check`` the call synchronises and raises if a request could not be
     resolved (such requests get -1 in both outputs).  ``timing_events``: an
-    optional ctypes array of 4 hipEvent_t recorded around the three kernels.
+    optional ctypes array of 4 hipEvent_t recorded around the kernels.
+    ``scan_hint``: 0 launches both row-scan kernels; 1 only the raw-logit
+    top-k scan (when every request uses top-k with repetition >= 1 and
+    non-negative frequency / presence); 2 only the exact scan.  A wrong hint
+    costs speed, never correctness.
     """
     what = "verify_sample"
     logits = _rows_view(logits, width, what)
@@ -239,6 +243,9 @@ def verify_sample(*, logits: torch.Tensor, candidates: torch.Tensor, width: int,
         final_uniforms.data_ptr()
     a.accept_lens, a.bonus, a.p_cand_out, a.status = accept.data_ptr(), bonus.data_ptr(), _lib.ptr(p_cand), \
         status.data_ptr()
+    if scan_hint not in (0, 1, 2):
+        raise ValueError(f"{what}: scan_hint must be 0, 1 or 2")
+    a.scan_hint = scan_hint
     if timing_events is not None:
         a.timing_events = _lib.ctypes.cast(timing_events, _lib.ctypes.c_void_p)
     cnt, scr = _lib.workspaces.get(*_lib.workspace_sizes("ls_verify_sample_workspace", batch, width, vocab, mk), dev)
