@@ -254,6 +254,135 @@ LS_API int ls_verify_sample_workspace(int64_t batch, int32_t width, int64_t voca
 LS_API int ls_verify_sample(const ls_verify_sample_args* args, void* counters, uint64_t counter_bytes,
                             void* scratch, uint64_t scratch_bytes, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * Recent-window page tables, window gather and ring append.
+ * ------------------------------------------------------------------------- */
+
+/* Raw256 page table: page_table[b, i] = req_to_token[slot_b, seq_b - raw_b + i]
+ * for i < raw_b = min(seq_b, window), 0 for i >= raw_b; raw_lengths[b] = raw_b
+ * (may be NULL).  req_to_token is int32 [slots, T] with element strides.
+ * Replaces SRT/speculative/global16_raw256_draft_fused.py:372-413
+ * (build_raw256_page_table, kernel :35-65) and the torch path
+ * SRT/speculative/global16_raw256.py:1343-1361. */
+LS_API int ls_raw_page_table(const int32_t* req_to_token, int64_t rtt_stride_b, int64_t rtt_stride_t,
+                             const void* req_pool_indices, int32_t slots_dtype, const void* seq_lens,
+                             int32_t seq_lens_dtype, int64_t batch, int32_t window, int32_t* page_table,
+                             int64_t page_table_stride, int32_t* raw_lengths, void* stream);
+
+/* Ring page table: pages[b, i] = slot_b * window + (len_b - raw_b + i) mod window,
+ * raw_b = min(len_b, window).  Replaces src/longspark/engine/draft.py:14-21
+ * (ring_page_table). */
+LS_API int ls_ring_page_table(const void* slots, int32_t slots_dtype, const void* lengths, int32_t lengths_dtype,
+                              int64_t batch, int32_t window, int32_t* pages, int64_t pages_stride,
+                              int32_t* raw_lengths, void* stream);
+
+/* Recent-window gather from a paged KV pool into a dense head-major view:
+ *   out[b, l, kv, h, i, :] = pool_kv[l][loc(b, seq_b - raw_b + i), h, :]  for i < raw_b,
+ *   zero for raw_b <= i < window,
+ * raw_b = min(seq_b, window), loc(b, t) = page_table[row_b, t / page_size] *
+ * page_size + t % page_size, row_b = table_rows[b] (NULL: b).  k_layers /
+ * v_layers are device arrays [n_layers] of per-layer base addresses; a
+ * token row is token_stride elements, heads head_stride apart (head rows,
+ * strides and output 16-byte aligned).  With page_size 1 and table_rows =
+ * req_pool_indices this reads req_to_token directly.
+ * Replaces the per-layer k[locations] export of src/longspark/engine/
+ * target.py:213-228 and the gather the page table of
+ * SRT/speculative/global16_raw256.py:1307-1361 feeds. */
+LS_API int ls_kv_window_gather(const uint64_t* k_layers, const uint64_t* v_layers, int32_t n_layers,
+                               int32_t dtype, int64_t token_stride, int64_t head_stride, int32_t heads,
+                               int32_t head_dim, const int32_t* page_table, int64_t page_table_stride,
+                               const void* table_rows, int32_t table_rows_dtype, int32_t page_size,
+                               const void* seq_lens, int32_t seq_lens_dtype, int64_t batch, int32_t window,
+                               void* out, int64_t out_stride_b, int64_t out_stride_l, int64_t out_stride_kv,
+                               int64_t out_stride_h, int64_t out_stride_w, int32_t* raw_lengths, void* stream);
+
+/* Ring append: for each request b, rows j < counts[b] of the packed source
+ * (row off_b + j, off_b = sum of earlier counts; or src_locs[off_b + j] when
+ * src_locs is given) are written to ring row
+ * slots[b] * window + (prev_lengths[b] + j) mod window of every layer, K and V.
+ * Layer bases are device arrays; row_bytes and both strides multiples of 16.
+ * Replaces src/longspark/engine/draft.py:207-212, 255-259 (self.keys[:,
+ * ring_locs] = keys) fused with the target-side row export of
+ * src/longspark/engine/target.py:213-228 (src_locs = the export locations). */
+LS_API int ls_ring_append(const uint64_t* src_k_layers, const uint64_t* src_v_layers, const uint64_t* dst_k_layers,
+                          const uint64_t* dst_v_layers, int32_t n_layers, int64_t row_bytes,
+                          int64_t src_row_stride_bytes, int64_t dst_row_stride_bytes, const void* src_locs,
+                          int32_t src_locs_dtype, const int32_t* slots, const int32_t* prev_lengths,
+                          const int32_t* counts, int64_t batch, int32_t window, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Summary (Global16) state: cached position scores and the online-softmax
+ * merge of accepted rows.
+ *
+ * Geometry: Hq query heads over Hkv KV heads (query head h uses KV head
+ * h / (Hq / Hkv)), S summary rows per query head, W new rows per request
+ * (W <= 32), head_dim D in {64, 128, 256}; queries, keys and values bf16 or
+ * fp16 (one dtype), scores / state / LSE fp32.  All element strides; the
+ * last (D) dimension is contiguous and rows of queries, keys and values are
+ * 16-byte aligned.
+ *
+ *   scores  s[b,h,r,w] = scale * sum_d q[b,h,r,d] k[b,w,h/g,d]
+ *           (softcap > 0: softcap * tanh(s / softcap)), fp32 accumulation;
+ *   merge   over w < len_b = accept_lens[b]:
+ *           d = logsumexp_w s, m = M + log(exp(lse - M) + exp(d - M)), M = max(lse, d),
+ *           out <- out * exp(lse - m) + sum_w exp(s_w - m) v[w], lse <- m,
+ *           on state row state_slots[b] (NULL: b); len_b <= 0 leaves the row unchanged.
+ *
+ * Replaces SRT/speculative/global16_raw256_incremental.py:400-456
+ * (cache_position_scores), :459-584 (merge_accepted_positions_) and the
+ * GQA-5 adapter src/longspark/patches/gqa5_attention.py:43-106; the fused
+ * update covers the per-layer score+merge loop of
+ * src/longspark/engine/draft.py:243-253 for all layers in one launch.
+ * ------------------------------------------------------------------------- */
+enum { LS_SUMMARY_SCORES = 1, LS_SUMMARY_MERGE = 2, LS_SUMMARY_UPDATE = 3 };
+
+/* Rows of a key or value source.  Layer l starts at layers[l] (device array)
+ * or, when layers is NULL, at base + l * stride_layer elements.  Row (b, w)
+ * of KV head h is at  loc * stride_loc + h * stride_h  when located (loc from
+ * the accepted-location table), else  b * stride_b + w * stride_w + h * stride_h. */
+typedef struct ls_kv_rows {
+  const void* base;
+  const uint64_t* layers;
+  int64_t stride_layer;
+  int64_t stride_b, stride_w;
+  int64_t stride_loc;
+  int64_t stride_h;
+  int32_t located;
+} ls_kv_rows;
+
+typedef struct ls_summary_args {
+  int64_t batch;
+  int32_t layers, q_heads, kv_heads, rows, width, head_dim;
+  int32_t dtype;                       /* LS_BF16 or LS_F16 */
+  float softmax_scale, softcap;
+  /* queries [L][B][Hq][S][D] (stride 0 over requests for a shared query) */
+  const void* query;
+  int64_t q_stride_l, q_stride_b, q_stride_h, q_stride_s;
+  ls_kv_rows keys, values;
+  /* scores [L][B][Hq][S][W] fp32: written by SCORES, read by MERGE, unused by UPDATE */
+  float* scores;
+  int64_t sc_stride_l, sc_stride_b, sc_stride_h, sc_stride_s, sc_stride_w;
+  /* state [C][L][Hq][S][D] and LSE [C][L][Hq][S] fp32, updated in place */
+  float* state_output;
+  int64_t so_stride_c, so_stride_l, so_stride_h, so_stride_s;
+  float* state_lse;
+  int64_t sl_stride_c, sl_stride_l, sl_stride_h, sl_stride_s;
+  const int32_t* state_slots;          /* [B] or NULL */
+  /* accepted cache locations: fixed [B][W] (element strides), or compact
+   * (flat; request b's rows at locs[off_b + w], off_b = sum of earlier
+   * accept_lens, written to accept_offsets[b] when accept_offsets is given) */
+  const void* locs;
+  int32_t locs_dtype;                  /* LS_I32 or LS_I64 */
+  int64_t locs_stride_b, locs_stride_w;
+  int32_t compact_locs;
+  int32_t* accept_offsets;
+  const int32_t* accept_lens;          /* [B] int32 */
+} ls_summary_args;
+
+LS_API int ls_summary_scores(const ls_summary_args* args, void* stream);
+LS_API int ls_summary_merge(const ls_summary_args* args, void* stream);
+LS_API int ls_summary_update(const ls_summary_args* args, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

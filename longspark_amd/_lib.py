@@ -57,6 +57,31 @@ class VerifySampleArgs(ctypes.Structure):
     ]
 
 
+class KvRows(ctypes.Structure):
+    """Mirror of ``ls_kv_rows``."""
+    _fields_ = [
+        ("base", P), ("layers", P), ("stride_layer", I64), ("stride_b", I64), ("stride_w", I64),
+        ("stride_loc", I64), ("stride_h", I64), ("located", I32),
+    ]
+
+
+class SummaryArgs(ctypes.Structure):
+    """Mirror of ``ls_summary_args``."""
+    _fields_ = [
+        ("batch", I64), ("layers", I32), ("q_heads", I32), ("kv_heads", I32), ("rows", I32), ("width", I32),
+        ("head_dim", I32), ("dtype", I32), ("softmax_scale", F32), ("softcap", F32),
+        ("query", P), ("q_stride_l", I64), ("q_stride_b", I64), ("q_stride_h", I64), ("q_stride_s", I64),
+        ("keys", KvRows), ("values", KvRows),
+        ("scores", P), ("sc_stride_l", I64), ("sc_stride_b", I64), ("sc_stride_h", I64), ("sc_stride_s", I64),
+        ("sc_stride_w", I64),
+        ("state_output", P), ("so_stride_c", I64), ("so_stride_l", I64), ("so_stride_h", I64), ("so_stride_s", I64),
+        ("state_lse", P), ("sl_stride_c", I64), ("sl_stride_l", I64), ("sl_stride_h", I64), ("sl_stride_s", I64),
+        ("state_slots", P),
+        ("locs", P), ("locs_dtype", I32), ("locs_stride_b", I64), ("locs_stride_w", I64), ("compact_locs", I32),
+        ("accept_offsets", P), ("accept_lens", P),
+    ]
+
+
 # name -> (restype, argtypes).  Kept in the order of include/longspark_amd.h.
 _SIGNATURES = {
     "ls_last_error": (c_char_p, []),
@@ -68,6 +93,14 @@ _SIGNATURES = {
     "ls_adjust_logits": (I32, [P, I32, I64, I64, I64, I32, P, P, I64, P, I64, P, I32, P, I64, I32, I64, P]),
     "ls_verify_sample_workspace": (I32, [I64, I32, I64, I32, P, P]),
     "ls_verify_sample": (I32, [ctypes.POINTER(VerifySampleArgs), P, U64, P, U64, P]),
+    "ls_raw_page_table": (I32, [P, I64, I64, P, I32, P, I32, I64, I32, P, I64, P, P]),
+    "ls_ring_page_table": (I32, [P, I32, P, I32, I64, I32, P, I64, P, P]),
+    "ls_kv_window_gather": (I32, [P, P, I32, I32, I64, I64, I32, I32, P, I64, P, I32, I32, P, I32, I64, I32,
+                                  P, I64, I64, I64, I64, I64, P, P]),
+    "ls_ring_append": (I32, [P, P, P, P, I32, I64, I64, I64, P, I32, P, P, P, I64, I32, P]),
+    "ls_summary_scores": (I32, [ctypes.POINTER(SummaryArgs), P]),
+    "ls_summary_merge": (I32, [ctypes.POINTER(SummaryArgs), P]),
+    "ls_summary_update": (I32, [ctypes.POINTER(SummaryArgs), P]),
 }
 
 for _name, (_res, _args) in _SIGNATURES.items():
