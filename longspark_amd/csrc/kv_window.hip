@@ -95,10 +95,22 @@ struct GatherArgs {
   int32_t* raw_out;
 };
 
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+
+// 16-byte non-temporal load through a pointer read from a layer table, marked
+// global so the compiler emits a global (not flat) load.
+__device__ __forceinline__ uint4 load16_global_stream(const char* p) {
+  const u32x4_t v = __builtin_nontemporal_load((const __attribute__((address_space(1))) u32x4_t*)(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 // One workgroup: kChunk window tokens of one (request, layer, K or V).
 // The chunk's physical rows are resolved once into LDS, then every thread
 // copies 16-byte vectors: (head h, window token i, vector c) with c fastest,
 // then i, so a wave writes contiguous runs of one head's output rows.
+// kVph = 16-byte vectors per head row when it is a power of two the kernel
+// was built for (index math by shifts), 0 = any (runtime division).
+template <int kVph>
 __global__ __launch_bounds__(kGT) void window_gather_kernel(GatherArgs a) {
   __shared__ int64_t locs[kChunk];
   const int chunks = (a.window + kChunk - 1) / kChunk;
@@ -126,27 +138,29 @@ __global__ __launch_bounds__(kGT) void window_gather_kernel(GatherArgs a) {
   __syncthreads();
   const char* src = reinterpret_cast<const char*>((kv ? a.v_layers : a.k_layers)[layer]);
   char* dst = a.out + (b * a.osb + layer * a.osl + kv * a.oskv) * a.esize;
-  const int vph = a.head_dim * a.esize / 16;  // 16-byte vectors per head row
+  const int vph = kVph ? kVph : a.head_dim * a.esize / 16;
   const int ntok = min(kChunk, a.window - i0);
-  const int per_head = ntok * vph;
+  const int per_head = kChunk * vph;   // tokens past ntok are skipped
   const int total = a.heads * per_head;
-  constexpr int kU = 4;
+  constexpr int kU = 8;
   for (int j0 = threadIdx.x; j0 < total; j0 += kGT * kU) {
     uint4 v[kU];
     char* dp[kU];
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
       const int j = j0 + u * kGT;
-      dp[u] = nullptr;
-      v[u] = make_uint4(0, 0, 0, 0);
-      if (j >= total) continue;
       const int h = j / per_head;
       const int r = j - h * per_head;
       const int ti = r / vph;
       const int c = r - ti * vph;
-      dp[u] = dst + (h * a.osh + static_cast<int64_t>(i0 + ti) * a.osw) * a.esize + c * 16;
-      const int64_t loc = locs[ti];
-      if (loc >= 0) v[u] = load16_stream(src + (loc * a.token_stride + h * a.head_stride) * a.esize + c * 16);
+      const bool live = j < total && ti < ntok;
+      const int64_t loc = live ? locs[ti] : -1;
+      dp[u] = live ? dst + (h * a.osh + static_cast<int64_t>(i0 + ti) * a.osw) * a.esize + c * 16 : nullptr;
+      // rows past raw and dead lanes read head 0 of row 0 (in bounds); rows
+      // past raw store zeros, dead lanes store nothing
+      v[u] = load16_global_stream(src + ((loc < 0 ? 0 : loc) * a.token_stride + (live ? h : 0) * a.head_stride) *
+                                            a.esize + c * 16);
+      if (loc < 0) v[u] = make_uint4(0, 0, 0, 0);
     }
 #pragma unroll
     for (int u = 0; u < kU; ++u)
@@ -273,7 +287,14 @@ extern "C" int ls_kv_window_gather(const uint64_t* k_layers, const uint64_t* v_l
   const int64_t chunks = (window + kChunk - 1) / kChunk;
   const int64_t grid = batch * n_layers * 2 * chunks;
   LS_CHECK(grid < (int64_t(1) << 31), LS_ERR_SHAPE, "ls_kv_window_gather: grid too large");
-  window_gather_kernel<<<dim3(static_cast<unsigned>(grid)), kGT, 0, static_cast<hipStream_t>(stream)>>>(a);
+  const dim3 g(static_cast<unsigned>(grid));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (head_dim * es / 16) {
+    case 8: window_gather_kernel<8><<<g, kGT, 0, st>>>(a); break;
+    case 16: window_gather_kernel<16><<<g, kGT, 0, st>>>(a); break;
+    case 32: window_gather_kernel<32><<<g, kGT, 0, st>>>(a); break;
+    default: window_gather_kernel<0><<<g, kGT, 0, st>>>(a); break;
+  }
   LS_LAUNCH_CHECK();
   return LS_OK;
 }

@@ -3,15 +3,17 @@
 //
 // One workgroup = 4 waves = one 64-row tile of the query rows that share a
 // KV head (rows r = g * S + s for the g-th query head of the group), for one
-// (layer, KV head, request).  The request index varies fastest and the
+// (layer, KV head, request); each lane owns one row.  The request index varies fastest and the
 // block -> unit mapping keeps consecutive units on one XCD, so the requests
 // that share a query tile (queries are shared across requests) read it from
 // the same L2.
 //
-//   scores  S[16 x 16] = Q[16 x D] . K^T[D x 16]   v_mfma_f32_16x16x32_{bf16,f16}
+//   scores  S^T[16 x 16] = K[16 x D] . Q^T[D x 16]   v_mfma_f32_16x16x32_{bf16,f16}
 //           (bf16/fp16 products are exact in fp32; fp32 accumulation);
-//   merge   O[16 x 16] = O * alpha + P[16 x W] . V[W x 16]   v_mfma_f32_16x16x4_f32
+//   merge   O^T[16 x 16] = O^T * alpha + V^T[16 x W] . P^T[W x 16]   v_mfma_f32_16x16x4_f32
 //           (P stays fp32: weights are not rounded to 16 bits).
+// Computing the transposed products leaves each lane with 4 consecutive
+// state values of one row, so the state moves with 16-byte loads and stores.
 // Reference math: SRT/speculative/global16_raw256_incremental.py:50-166 and
 // the kernel forms :172-238 (scores) and :258-392 (merge, including its
 // M + log(exp(lse - M) + exp(d - M)) LSE update);
@@ -74,28 +76,46 @@ __device__ __forceinline__ float sum16(float v) {
   return v;
 }
 
-// Stage rows w < nrows of a key/value source into LDS; rows nrows..wpad-1 are zero.
-// Keys keep their 16-bit pattern (pitch kp elements), values are widened to fp32.
-template <int D, typename Tag, bool kWiden>
-__device__ __forceinline__ void stage_rows(const ls_summary_args& a, const ls_kv_rows& src, int layer, int64_t b,
-                                           int kvh, int nrows, int wpad, int64_t loc_off, void* lds, int pitch) {
+// Workgroup barrier that orders LDS only: outstanding global loads stay in
+// flight across it (a full __syncthreads would wait for them).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// 16-byte load through a pointer read from memory (layer tables), marked as
+// global so the compiler emits a global (not flat) load.
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 load16_global(const char* p) {
+  const u32x4_t v = *(const __attribute__((address_space(1))) u32x4_t*)(p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// Stage rows w < nrows of the keys (kept as 16-bit patterns, pitch kp) and/or
+// values (widened to fp32, pitch vp) into LDS; rows nrows..wpad-1 are zero.
+// koff / voff hold each row's element offset within its layer.
+template <int D, typename Tag, bool kKeys, bool kValues>
+__device__ __forceinline__ void stage_rows(const char* kbase, const char* vbase, const int64_t* koff,
+                                           const int64_t* voff, int nrows, int wpad, uint16_t* kls, int kp,
+                                           float* vls, int vp) {
   constexpr int kVecs = D / 8;
-  const char* base = layer_base(src, layer);
   for (int j = threadIdx.x; j < wpad * kVecs; j += kSumThreads) {
     const int w = j / kVecs, c = j - w * kVecs;
-    uint4 v = make_uint4(0, 0, 0, 0);
-    if (w < nrows) {
-      const int64_t loc = src.located ? load_loc(a, b, w, loc_off) : 0;
-      v = load16(base + (row_offset(src, b, w, loc, kvh) + c * 8) * 2);
+    uint4 kv = make_uint4(0, 0, 0, 0), vv = make_uint4(0, 0, 0, 0);
+    if (kKeys) kv = load16_global(kbase + (koff[w] + c * 8) * 2);
+    if (kValues) vv = load16_global(vbase + (voff[w] + c * 8) * 2);
+    if (w >= nrows) {
+      kv = make_uint4(0, 0, 0, 0);
+      vv = make_uint4(0, 0, 0, 0);
     }
-    if constexpr (kWiden) {
+    if (kKeys) *reinterpret_cast<uint4*>(kls + w * kp + c * 8) = kv;
+    if (kValues) {
       float f[8];
-      unpack16<Tag>(v, f);
-      float4* dst = reinterpret_cast<float4*>(static_cast<float*>(lds) + w * pitch + c * 8);
+      unpack16<Tag>(vv, f);
+      float4* dst = reinterpret_cast<float4*>(vls + w * vp + c * 8);
       dst[0] = make_float4(f[0], f[1], f[2], f[3]);
       dst[1] = make_float4(f[4], f[5], f[6], f[7]);
-    } else {
-      *reinterpret_cast<uint4*>(static_cast<uint16_t*>(lds) + w * pitch + c * 8) = v;
     }
   }
 }
@@ -107,14 +127,11 @@ __global__ __launch_bounds__(kSumThreads) void summary_kernel(const ls_summary_a
   constexpr int kKB = D / 32;      // 32-deep steps of the score product
   constexpr int kDB = D / 16;      // 16-column blocks of the state
   constexpr int kKPitch = D + 8;   // 16-bit elements per LDS key row
-  constexpr int kVPitch = D + 16;  // fp32 per LDS value row (conflict-free B reads)
+  constexpr int kVPitch = D + 4;   // fp32 per LDS value row: rows 4 apart land 16 banks apart
   extern __shared__ __align__(16) char smem[];
-  __shared__ int s_len;
-  __shared__ int64_t s_off;
+  __shared__ int64_t s_koff[kMaxWidth], s_voff[kMaxWidth];
   uint16_t* kls = reinterpret_cast<uint16_t*>(smem);
   float* vls = reinterpret_cast<float*>(smem + (kScore ? wpad * kKPitch * 2 : 0));
-  float* pls = vls + (kMerge ? wpad * kVPitch : 0);
-  const int ppitch = wpad + 1;
 
   // XCD-aware unit: blocks are dispatched round-robin over 8 XCDs; give each
   // XCD a contiguous range of units.
@@ -128,101 +145,90 @@ __global__ __launch_bounds__(kSumThreads) void summary_kernel(const ls_summary_a
   const int kvh = static_cast<int>(u % a.kv_heads);
   const int layer = static_cast<int>(u / a.kv_heads);
   const int groups = a.q_heads / a.kv_heads;
-  const int nrows_total = groups * a.rows;
-  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int lane = threadIdx.x % kWave;
   const int g16 = lane >> 4, c16 = lane & 15;
-  const int r0 = tile * kTileRows + wave * 16;
+  // Each lane owns one query row (c16 of its wave's 16) in every product below:
+  //   S^T[w][r] = K[w] . Q[r]    lane holds w = nt*16 + 4*g16 + i,
+  //   O^T[d][r] += V^T[d][w] P^T[w][r]   lane holds d = db*16 + 4*g16 + i,
+  // so its state values are 4 consecutive floats of its row.
+  const int r = tile * kTileRows + (threadIdx.x / kWave) * 16 + c16;
+  const bool valid = r < groups * a.rows;
+  const int rr = valid ? r : 0;
+  const int head = kvh * groups + rr / a.rows, srow = rr % a.rows;
 
   int len = a.width;
-  int64_t loc_off = 0;
-  if (kMerge || a.keys.located) {
-    if (threadIdx.x < kWave) {
-      int64_t off = 0;
-      if (a.compact_locs) {
-        for (int64_t j = lane; j < b; j += kWave) off += a.accept_lens[j];
-#pragma unroll
-        for (int o = kWave / 2; o > 0; o >>= 1) off += __shfl_xor(off, o, kWave);
-      }
-      if (lane == 0) {
-        int l = kMerge ? a.accept_lens[b] : a.width;
-        s_len = l < 0 ? 0 : (l > a.width ? a.width : l);
-        s_off = off;
-        if (a.compact_locs && a.accept_offsets && layer == 0 && kvh == 0 && tile == 0)
-          a.accept_offsets[b] = static_cast<int32_t>(off);
-      }
-    }
-    __syncthreads();
-    len = s_len;
-    loc_off = s_off;
-    if (kMerge && len <= 0) return;  // uniform over the workgroup
+  if (kMerge) {
+    const int l = a.accept_lens[b];
+    len = l < 0 ? 0 : (l > a.width ? a.width : l);
   }
+  int64_t loc_off = 0;
+  if (a.compact_locs && (kMerge || a.keys.located)) {
+    for (int64_t j = lane; j < b; j += kWave) loc_off += a.accept_lens[j];
+#pragma unroll
+    for (int o = kWave / 2; o > 0; o >>= 1) loc_off += __shfl_xor(loc_off, o, kWave);
+    if (a.accept_offsets && threadIdx.x == 0 && layer == 0 && kvh == 0 && tile == 0)
+      a.accept_offsets[b] = static_cast<int32_t>(loc_off);
+  }
+  if (kMerge && len <= 0) return;  // uniform over the workgroup
   const int wl = kMerge ? len : a.width;  // key/value rows that take part
 
-  // Rows this lane holds in the MFMA result layout: r0 + 4*g16 + i.
-  int head_i[4], srow_i[4];
-  bool valid_i[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = r0 + 4 * g16 + i;
-    valid_i[i] = r < nrows_total;
-    const int rr = valid_i[i] ? r : 0;
-    head_i[i] = kvh * groups + rr / a.rows;
-    srow_i[i] = rr % a.rows;
+  // Row offsets of the staged key/value rows (rows past wl repeat row wl-1,
+  // a valid address; their data is zeroed when staged).
+  if (threadIdx.x < wpad) {
+    const int wr = static_cast<int>(threadIdx.x) < wl ? static_cast<int>(threadIdx.x) : wl - 1;
+    const bool need_loc = (kScore && a.keys.located) || (kMerge && a.values.located);
+    const int64_t loc = need_loc ? load_loc(a, b, wr, loc_off) : 0;
+    if (kScore) s_koff[threadIdx.x] = row_offset(a.keys, b, wr, loc, kvh);
+    if (kMerge) s_voff[threadIdx.x] = row_offset(a.values, b, wr, loc, kvh);
   }
 
-  // State and prior LSE (issued first: they are the bulk of the traffic).
-  f32x4_t acc[kDB];
-  float prior[4];
-  float* so_row[4];
-  float* sl_ptr[4];
+  // State row and prior LSE (the bulk of the traffic; issued first).
+  f32x4_t o[kMerge ? kDB : 1];
+  float prior = 0.f;
+  float* so_row = nullptr;
+  float* sl_ptr = nullptr;
   if constexpr (kMerge) {
     const int64_t slot = a.state_slots ? a.state_slots[b] : b;
+    so_row = a.state_output + slot * a.so_stride_c + layer * a.so_stride_l + head * a.so_stride_h +
+             srow * a.so_stride_s + 4 * g16;
+    sl_ptr = a.state_lse + slot * a.sl_stride_c + layer * a.sl_stride_l + head * a.sl_stride_h +
+             srow * a.sl_stride_s;
+    // Lanes past the last row read row 0 (a valid address) and never store.
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      so_row[i] = a.state_output + slot * a.so_stride_c + layer * a.so_stride_l + head_i[i] * a.so_stride_h +
-                  srow_i[i] * a.so_stride_s;
-      sl_ptr[i] = a.state_lse + slot * a.sl_stride_c + layer * a.sl_stride_l + head_i[i] * a.sl_stride_h +
-                  srow_i[i] * a.sl_stride_s;
-      prior[i] = valid_i[i] ? *sl_ptr[i] : 0.f;
-    }
-#pragma unroll
-    for (int db = 0; db < kDB; ++db)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) acc[db][i] = valid_i[i] ? so_row[i][db * 16 + c16] : 0.f;
+    for (int db = 0; db < kDB; ++db) o[db] = *reinterpret_cast<const f32x4_t*>(so_row + db * 16);
+    prior = *sl_ptr;
   }
 
-  // Query rows in the MFMA A layout: row r0 + c16, depth 8*g16.. of each 32-step.
-  uint4 qa[kScore ? kKB : 1];
+  // Query row as the B operand of S^T: depth 8*g16.. of each 32-step.
+  uint4 qb[kScore ? kKB : 1];
   if constexpr (kScore) {
-    const int r = r0 + c16;
-    if (r < nrows_total) {
-      const int h = kvh * groups + r / a.rows, s = r % a.rows;
-      const char* q = static_cast<const char*>(a.query) +
-                      (layer * a.q_stride_l + b * a.q_stride_b + h * a.q_stride_h + s * a.q_stride_s) * 2;
+    const char* q = static_cast<const char*>(a.query) +
+                    (layer * a.q_stride_l + b * a.q_stride_b + head * a.q_stride_h + srow * a.q_stride_s) * 2;
 #pragma unroll
-      for (int kb = 0; kb < kKB; ++kb) qa[kb] = load16(q + (kb * 32 + g16 * 8) * 2);
-    } else {
-#pragma unroll
-      for (int kb = 0; kb < kKB; ++kb) qa[kb] = make_uint4(0, 0, 0, 0);
-    }
-    stage_rows<D, Tag, false>(a, a.keys, layer, b, kvh, wl, wpad, loc_off, kls, kKPitch);
+    for (int kb = 0; kb < kKB; ++kb) qb[kb] = load16(q + (kb * 32 + g16 * 8) * 2);
   }
-  if constexpr (kMerge) stage_rows<D, Tag, true>(a, a.values, layer, b, kvh, wl, wpad, loc_off, vls, kVPitch);
-  __syncthreads();
+  lds_barrier();
+  stage_rows<D, Tag, kScore, kMerge>(kScore ? layer_base(a.keys, layer) : nullptr,
+                                     kMerge ? layer_base(a.values, layer) : nullptr, s_koff, s_voff, wl, wpad, kls,
+                                     kKPitch, vls, kVPitch);
+  lds_barrier();
 
-  // Scores: sc[nt][i] = S[r0 + 4*g16 + i][nt*16 + c16].
+  // Scores of this lane's row: sc[nt][i] = S[r][nt*16 + 4*g16 + i].
   const int wtiles = wpad / 16;
   f32x4_t sc[kMaxWidth / 16];
+  const float* sc_row = nullptr;
+  if (kMode != LS_SUMMARY_UPDATE)
+    sc_row = a.scores + layer * a.sc_stride_l + b * a.sc_stride_b + head * a.sc_stride_h + srow * a.sc_stride_s;
 #pragma unroll
   for (int nt = 0; nt < kMaxWidth / 16; ++nt) {
     if (nt >= wtiles) break;
-    const int w = nt * 16 + c16;
+    const int w0 = nt * 16 + 4 * g16;
     if constexpr (kScore) {
       f32x4_t t = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kb = 0; kb < kKB; ++kb) {
-        const uint4 kv = *reinterpret_cast<const uint4*>(kls + w * kKPitch + kb * 32 + g16 * 8);
-        t = Mma<Tag>::run(qa[kb], kv, t);
+        const uint4 kv = *reinterpret_cast<const uint4*>(kls + (nt * 16 + c16) * kKPitch + kb * 32 + g16 * 8);
+        t = Mma<Tag>::run(kv, qb[kb], t);
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -234,68 +240,59 @@ __global__ __launch_bounds__(kSumThreads) void summary_kernel(const ls_summary_a
     } else {
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        sc[nt][i] = (valid_i[i] && w < len)
-                        ? a.scores[layer * a.sc_stride_l + b * a.sc_stride_b + head_i[i] * a.sc_stride_h +
-                                   srow_i[i] * a.sc_stride_s + w * a.sc_stride_w]
-                        : -__builtin_inff();
+        sc[nt][i] = (valid && w0 + i < len) ? sc_row[(w0 + i) * a.sc_stride_w] : -__builtin_inff();
     }
     if constexpr (kMode == LS_SUMMARY_SCORES) {
-      if (w < a.width) {
+      float* out = const_cast<float*>(sc_row);
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (valid_i[i])
-            a.scores[layer * a.sc_stride_l + b * a.sc_stride_b + head_i[i] * a.sc_stride_h +
-                     srow_i[i] * a.sc_stride_s + w * a.sc_stride_w] = sc[nt][i];
-      }
+      for (int i = 0; i < 4; ++i)
+        if (valid && w0 + i < a.width) out[(w0 + i) * a.sc_stride_w] = sc[nt][i];
     }
   }
   if constexpr (!kMerge) return;
 
-  // Online-softmax merge of the rows w < len.
-  float alpha[4], merged[4];
+  // Online-softmax merge of the rows w < len: each row's 16*wtiles scores sit
+  // in the 4 lanes that share c16.
+  float m = -__builtin_inff();
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    float m = -__builtin_inff();
+  for (int nt = 0; nt < kMaxWidth / 16; ++nt)
 #pragma unroll
-    for (int nt = 0; nt < kMaxWidth / 16; ++nt)
-      if (nt < wtiles && nt * 16 + c16 < len) m = fmaxf(m, sc[nt][i]);
-    m = max16(m);
-    float z = 0.f;
+    for (int i = 0; i < 4; ++i)
+      if (nt < wtiles && nt * 16 + 4 * g16 + i < len) m = fmaxf(m, sc[nt][i]);
+  m = fmaxf(m, __shfl_xor(m, 16, kWave));
+  m = fmaxf(m, __shfl_xor(m, 32, kWave));
+  float z = 0.f;
 #pragma unroll
-    for (int nt = 0; nt < kMaxWidth / 16; ++nt)
-      if (nt < wtiles && nt * 16 + c16 < len) z += expf(sc[nt][i] - m);
-    z = sum16(z);
-    const float delta = m + logf(z);
-    const float big = fmaxf(prior[i], delta);
-    merged[i] = big + logf(expf(prior[i] - big) + expf(delta - big));
-    alpha[i] = expf(prior[i] - merged[i]);
+  for (int nt = 0; nt < kMaxWidth / 16; ++nt)
 #pragma unroll
-    for (int nt = 0; nt < kMaxWidth / 16; ++nt) {
-      if (nt >= wtiles) break;
-      const int w = nt * 16 + c16;
-      const float p = (valid_i[i] && w < len) ? expf(sc[nt][i] - merged[i]) : 0.f;
-      pls[(wave * 16 + 4 * g16 + i) * ppitch + w] = p;
+    for (int i = 0; i < 4; ++i)
+      if (nt < wtiles && nt * 16 + 4 * g16 + i < len) z += expf(sc[nt][i] - m);
+  z += __shfl_xor(z, 16, kWave);
+  z += __shfl_xor(z, 32, kWave);
+  const float delta = m + logf(z);
+  const float big = fmaxf(prior, delta);
+  const float merged = big + logf(expf(prior - big) + expf(delta - big));
+  const float alpha = expf(prior - merged);
+#pragma unroll
+  for (int db = 0; db < kDB; ++db) o[db] *= alpha;
+  // k step ks of tile nt pairs lane (g16, c16) with w = nt*16 + 4*g16 + ks on both operands.
+#pragma unroll
+  for (int nt = 0; nt < kMaxWidth / 16; ++nt) {
+    if (nt >= wtiles || nt * 16 >= len) break;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const int w = nt * 16 + 4 * g16 + ks;
+      const float pb = (valid && w < len) ? expf(sc[nt][ks] - merged) : 0.f;
+      const float* vrow = vls + w * kVPitch + c16;
+#pragma unroll
+      for (int db = 0; db < kDB; ++db) o[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vrow[db * 16], pb, o[db], 0, 0, 0);
     }
   }
-  __syncthreads();
+  if (!valid) return;
 #pragma unroll
   for (int db = 0; db < kDB; ++db)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) acc[db][i] *= alpha[i];
-  const int ksteps = (len + 3) / 4;
-  for (int ks = 0; ks < ksteps; ++ks) {
-    const float pa = pls[(wave * 16 + c16) * ppitch + 4 * ks + g16];
-    const float* vrow = vls + (4 * ks + g16) * kVPitch + c16;
-#pragma unroll
-    for (int db = 0; db < kDB; ++db) acc[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa, vrow[db * 16], acc[db], 0, 0, 0);
-  }
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    if (!valid_i[i]) continue;
-#pragma unroll
-    for (int db = 0; db < kDB; ++db) so_row[i][db * 16 + c16] = acc[db][i];
-    if (c16 == 0) *sl_ptr[i] = merged[i];
-  }
+    *reinterpret_cast<f32x4_t*>(so_row + db * 16) = o[db];
+  if (g16 == 0) *sl_ptr = merged;
 }
 
 template <int D, int kMode>
@@ -340,6 +337,9 @@ int summary_entry(const ls_summary_args* ap, void* stream, const char* what) {
     LS_CHECK(a.state_output && a.state_lse && a.accept_lens && (a.values.base || a.values.layers), LS_ERR_VALUE,
              "%s: state, LSE, accept_lens and values are required", what);
     LS_CHECK(rows_aligned(a.values), LS_ERR_ALIGN, "%s: value rows must be 16-byte aligned", what);
+    LS_CHECK(aligned16(a.state_output) && (a.so_stride_c * 4) % 16 == 0 && (a.so_stride_l * 4) % 16 == 0 &&
+                 (a.so_stride_h * 4) % 16 == 0 && (a.so_stride_s * 4) % 16 == 0,
+             LS_ERR_ALIGN, "%s: state rows must be 16-byte aligned", what);
   }
   const bool need_locs = (kMerge && a.values.located) || (kScore && a.keys.located);
   if (need_locs) {
@@ -356,7 +356,7 @@ int summary_entry(const ls_summary_args* ap, void* stream, const char* what) {
   LS_CHECK(grid < (int64_t(1) << 31), LS_ERR_SHAPE, "%s: grid too large", what);
   const int d = a.head_dim;
   const size_t lds = (kScore ? static_cast<size_t>(wpad) * (d + 8) * 2 : 0) +
-                     (kMerge ? static_cast<size_t>(wpad) * (d + 16) * 4 + kTileRows * (wpad + 1) * 4 : 0);
+                     (kMerge ? static_cast<size_t>(wpad) * (d + 4) * 4 : 0);
   hipStream_t st = static_cast<hipStream_t>(stream);
   switch (d) {
     case 64: return launch_d<64, kMode>(a, tiles, wpad, lds, grid, st);
