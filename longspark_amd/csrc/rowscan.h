@@ -79,8 +79,8 @@ __device__ __forceinline__ float transform1(const XForm& f, float x, int64_t v) 
   if (f.pbits) {
     const uint32_t word = f.pbits[w];
     if (word & bit) {
-      const uint32_t rank = f.prank[w] + __popc(word & (bit - 1u));
-      x = penalise(x, f.padd ? f.padd[rank] : 0.f, f.rep, f.quirk);
+      const float a = f.padd ? f.padd[f.prank[w] + __popc(word & (bit - 1u))] : 0.f;
+      x = penalise(x, a, f.rep, f.quirk);
     }
   }
   if (f.mbits && !(f.mbits[w] & bit)) x = -INFINITY;
@@ -97,14 +97,19 @@ __device__ __forceinline__ void transform_vec(const XForm& f, float* x, int64_t 
     const uint32_t word = f.pbits[w];
     uint32_t hit = (word >> sh) & lanes;
     if (hit) {
-      const uint32_t base = f.prank[w] + __popc(word & ((1u << sh) - 1u));
-      uint32_t rank = base;
+      if (f.padd) {
+        uint32_t rank = f.prank[w] + __popc(word & ((1u << sh) - 1u));
 #pragma unroll
-      for (int k = 0; k < P; ++k) {
-        if ((hit >> k) & 1u) {
-          x[k] = penalise(x[k], f.padd ? f.padd[rank] : 0.f, f.rep, f.quirk);
-          ++rank;
+        for (int k = 0; k < P; ++k) {
+          if ((hit >> k) & 1u) {
+            x[k] = penalise(x[k], f.padd[rank], f.rep, f.quirk);
+            ++rank;
+          }
         }
+      } else {
+#pragma unroll
+        for (int k = 0; k < P; ++k)
+          if ((hit >> k) & 1u) x[k] = penalise(x[k], 0.f, f.rep, f.quirk);
       }
     }
   }

@@ -20,6 +20,7 @@
 // .../speculative/dflash_utils.py:743-810 plus min-p, and the draft-probs
 // ("dense q") acceptance of .../speculative/reject_sampling.py:5-156.
 #include "rowscan.h"
+#include <stdlib.h>
 
 namespace ls {
 namespace {
@@ -93,11 +94,18 @@ struct Args {
   uint64_t* pubs_t;   // [B*K, S_t, 2]
   uint64_t* pub_d;    // [B, kNBuf]
   uint64_t* pubs_d;   // [B, S_d, 2]
+  struct CandRec* cand_rec;  // [B*K] transformed logit of each row's drafted token
   int hint;            // which scan kernels the launcher runs (Hint)
   uint32_t* list_cnt;  // counters [2]: rows waiting for the exact fallback (target, draft)
   int32_t* list_t;     // [B*K]
   int32_t* list_d;     // [B]
   int s_t, s_d;
+};
+
+// Drafted token of a target row and its transformed logit (tok < 0: none).
+struct CandRec {
+  float x;
+  int tok;
 };
 
 __device__ __forceinline__ void atomic_put_u64(uint64_t* p, uint64_t v) {
@@ -128,23 +136,32 @@ enum Why : int {
   kWhyExact = 256,    // record written by the fallback
 };
 
-// k-th largest (ties counted) of the kT values v (one per thread), k <= kT.
+// A lower bound of the k-th largest (ties counted) of the kT values v (one
+// per thread), k <= kT: each wave sorts its 64 values with a bitonic network
+// of lane shuffles and takes its ceil(k / waves)-th largest; at least k of
+// the values are >= the smallest of those, so it is a valid lower bound.
 __device__ __forceinline__ float kth_largest_of_block(Shared& sh, float v, int k) {
-  float* vals = reinterpret_cast<float*>(sh.hist);  // kT floats
-  __shared__ float res;
-  const int tid = threadIdx.x;
-  vals[tid] = v;
-  if (tid == 0) res = -INFINITY;
-  __syncthreads();
-  int gt = 0, ge = 0;
-  for (int j = 0; j < kT; ++j) {
-    const float w = vals[j];
-    gt += w > v;
-    ge += w >= v;
+  constexpr int kWaves = kT / kWave;
+  const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+#pragma unroll
+  for (int size = 2; size <= kWave; size <<= 1) {
+#pragma unroll
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      const float o = __shfl_xor(v, stride, kWave);
+      // descending blocks keep the maximum in the lower lane of each pair
+      const bool desc = (lane & size) == 0 || size == kWave;
+      const bool lower = (lane & stride) == 0;
+      v = (lower == desc) ? fmaxf(v, o) : fminf(v, o);
+    }
   }
-  if (gt < k && k <= ge) res = v;  // every writer holds the same value
+  const int j = (k + kWaves - 1) / kWaves;  // 1 <= j <= 64
+  const float wj = __shfl(v, j - 1, kWave);
   __syncthreads();
-  const float r = res;
+  if (lane == 0) sh.red_f[wid] = wj;
+  __syncthreads();
+  float r = sh.red_f[0];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) r = fminf(r, sh.red_f[w]);
   __syncthreads();
   return r;
 }
@@ -210,7 +227,7 @@ __device__ __forceinline__ void load_slot(Slot& s, const uint4* vp, int64_t i, i
     const int64_t w = (b + i * P) >> 5;
     if (f.pbits) {
       s.pb = f.pbits[w];
-      s.pr = f.prank[w];
+      if (f.padd) s.pr = f.prank[w];  // ranks only index additive values
     }
     if (f.mbits) s.mb = f.mbits[w];
   }
@@ -470,14 +487,24 @@ __device__ ScanOut scan_topk_raw(Shared& sh, const typename Tag::storage* row, i
     // four transformed vectors is a lower bound of the row's k-th largest
     // transformed value.
     float lm = -INFINITY, rm = -INFINITY;
+    // Penalty and mask words of the four vectors, all requested at once.
+    Slot w4[4];
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      const int64_t w = (b + (static_cast<int64_t>(d) * kT + tid) * P) >> 5;
+      w4[d].pb = f.pbits ? f.pbits[w] : 0u;
+      w4[d].pr = (f.pbits && f.padd) ? f.prank[w] : 0u;
+      w4[d].mb = f.mbits ? f.mbits[w] : ~0u;
+    }
 #pragma unroll 1
     for (int d = 0; d < 4; ++d) {
       const uint4 v = d == 0 ? r0 : d == 1 ? r1 : d == 2 ? r2 : r3;
+      const Slot& wd = d == 0 ? w4[0] : d == 1 ? w4[1] : d == 2 ? w4[2] : w4[3];
       float x[P];
       unpack16<Tag>(v, x);
 #pragma unroll
       for (int q = 0; q < P; ++q) rm = fmaxf(rm, x[q]);
-      if (f.pbits || f.mbits) transform_vec<P>(f, x, b + (static_cast<int64_t>(d) * kT + tid) * P);
+      if (f.pbits || f.mbits) transform_words<P>(f, x, b + (static_cast<int64_t>(d) * kT + tid) * P, wd);
 #pragma unroll
       for (int q = 0; q < P; ++q) lm = fmaxf(lm, x[q]);
     }
@@ -1110,6 +1137,27 @@ __device__ __forceinline__ XForm target_xform(const Args& a, int64_t b, int64_t 
 
 // --------------------------------------------------------------- kernels ---
 
+// One thread per target row: the drafted token checked at this row and its
+// logit after penalties and mask (the rows' scans need it only at the end).
+template <typename TagT, typename CandT>
+__global__ __launch_bounds__(kT) void cand_prep_kernel(Args a) {
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * kT + threadIdx.x;
+  if (row >= a.batch * a.width) return;
+  const int64_t b = row / a.width;
+  const int j = static_cast<int>(row % a.width);
+  CandRec cr{NAN, -1};
+  if (j < a.width - 1) {
+    const int64_t c = cand_at<CandT>(a, b, j);
+    if (c >= 0 && c < a.vocab) {
+      using S = typename TagT::storage;
+      const S* rp = static_cast<const S*>(a.logits) + row * a.lrs;
+      cr.tok = static_cast<int>(c);
+      cr.x = transform1(target_xform(a, b, row), to_f32<S>(rp[c]), c);
+    }
+  }
+  a.cand_rec[row] = cr;
+}
+
 template <typename TagT, bool kVec, typename CandT, int kPath>
 __global__ __launch_bounds__(kT) void target_scan_kernel(Args a) {
   __shared__ Shared sh;
@@ -1122,45 +1170,65 @@ __global__ __launch_bounds__(kT) void target_scan_kernel(Args a) {
   using S = typename TagT::storage;
   const S* rp = static_cast<const S*>(a.logits) + row * a.lrs;
   const XForm f = target_xform(a, b, row);
-  int cand_tok = -1;
-  float cand_x = NAN;
-  if (j < a.width - 1) {
-    const int64_t c = cand_at<CandT>(a, b, j);
-    if (c >= 0 && c < a.vocab) {
-      cand_tok = static_cast<int>(c);
-      cand_x = transform1(f, to_f32<S>(rp[c]), c);
-    }
-  }
+  // Drafted token and its transformed logit, prepared by cand_prep_kernel
+  // (a dependent chain of loads kept off the scan's critical path).
+  const CandRec cr = a.cand_rec[row];
   process_row<TagT, kVec, kPath>(sh, rp, a.vocab, p, f, a.s_t, slice, a.pub_t + row * kNBuf,
                                  a.pubs_t + row * a.s_t * 2, a.cnt_t + row, a.rec_t + row,
-                                 a.sidx_t + row * kCap, a.sp_t + row * kCap, cand_tok, cand_x, a.list_cnt,
+                                 a.sidx_t + row * kCap, a.sp_t + row * kCap, cr.tok, cr.x, a.list_cnt,
                                  a.list_t, static_cast<int32_t>(row), raw_filter_ok(f, a.pnonpos, b), a.hint);
 }
 
 // First rejected position of request b (width-1 when every drafted token is
-// accepted), from the target row records.  Also reports blocking flags.
+// accepted) and blocking flags, from the target row records.  Called by all
+// 64 lanes of one wave (lane j tests position j); every lane gets the result.
 template <typename CandT>
-__device__ int accept_length(const Args& a, int64_t b, int* flags) {
+__device__ int accept_length_wave(const Args& a, int64_t b, int* flags) {
   const int g = a.width - 1;
-  int len = 0;
-  *flags = 0;
-  for (; len < g; ++len) {
-    const RowRec& r = a.rec_t[b * a.width + len];
-    if (r.flags & kFlagOverflow) { *flags = r.flags; return len; }
-    float q;
-    if (a.q_mode == 0) {
-      q = a.dtp[b * a.dtp_sb + len];
-    } else {
-      const int64_t c = cand_at<CandT>(a, b, len);
-      q = (c >= 0 && c < a.vocab)
-              ? static_cast<const float*>(a.draft)[b * a.dsb + static_cast<int64_t>(len) * a.dsk + c]
-              : 0.f;
+  const int lane = threadIdx.x & (kWave - 1);
+  for (int base = 0; base < g; base += kWave) {
+    const int j = base + lane;
+    bool ok = false;
+    int fl = 0;
+    if (j < g) {
+      const RowRec& r = a.rec_t[b * a.width + j];
+      fl = r.flags;
+      if (!(fl & kFlagOverflow)) {
+        float q;
+        if (a.q_mode == 0) {
+          q = a.dtp[b * a.dtp_sb + j];
+        } else {
+          const int64_t c = cand_at<CandT>(a, b, j);
+          q = (c >= 0 && c < a.vocab)
+                  ? static_cast<const float*>(a.draft)[b * a.dsb + static_cast<int64_t>(j) * a.dsk + c]
+                  : 0.f;
+        }
+        ok = a.uni[b * a.usb + j] * q < r.p_cand;
+      }
     }
-    const float u = a.uni[b * a.usb + len];
-    if (!(u * q < r.p_cand)) break;
+    const uint64_t fail = __ballot(j < g && !ok);
+    if (fail) {
+      const int first = __ffsll(static_cast<long long>(fail)) - 1;
+      const int ff = __shfl(fl, first, kWave);
+      *flags = (ff & kFlagOverflow) ? ff : 0;
+      return base + first;
+    }
   }
-  if (a.rec_t[b * a.width + len].flags & kFlagOverflow) *flags = kFlagOverflow;
-  return len;
+  *flags = (a.rec_t[b * a.width + g].flags & kFlagOverflow) ? kFlagOverflow : 0;
+  return g;
+}
+
+// Wave 0 computes the accepted length into s_len / s_flags (all threads call).
+template <typename CandT>
+__device__ __forceinline__ void accept_length_block(const Args& a, int64_t b, int* s_len, int* s_flags) {
+  if (threadIdx.x < kWave) {
+    int fl;
+    const int len = accept_length_wave<CandT>(a, b, &fl);
+    if (threadIdx.x == 0) {
+      *s_len = len;
+      *s_flags = fl;
+    }
+  }
 }
 
 template <typename TagD, bool kVec, typename CandT, int kPath>
@@ -1169,7 +1237,7 @@ __global__ __launch_bounds__(kT) void draft_scan_kernel(Args a) {
   __shared__ int s_len, s_flags;
   const int64_t b = blockIdx.x / a.s_d;
   const int slice = blockIdx.x % a.s_d;
-  if (threadIdx.x == 0) s_len = accept_length<CandT>(a, b, &s_flags);
+  accept_length_block<CandT>(a, b, &s_len, &s_flags);
   __syncthreads();
   const int len = s_len;
   if (len >= a.width - 1 || s_flags) {
@@ -1232,28 +1300,19 @@ __global__ __launch_bounds__(kT) void target_fallback_kernel(Args a) {
   for (uint32_t li = blockIdx.x; li < n; li += gridDim.x) {
     const int64_t row = a.list_t[li];
     const int64_t b = row / a.width;
-    const int j = static_cast<int>(row % a.width);
     const RowRec prev = a.rec_t[row];
     Params p{a.temps[b], a.top_ks ? max(a.top_ks[b], 1) : static_cast<int>(a.vocab),
              a.top_ps ? a.top_ps[b] : 1.f, a.min_ps ? a.min_ps[b] : 0.f};
     using S = typename TagT::storage;
     const S* rp = static_cast<const S*>(a.logits) + row * a.lrs;
     const XForm f = target_xform(a, b, row);
-    int cand_tok = -1;
-    float cand_x = NAN;
-    if (j < a.width - 1) {
-      const int64_t c = cand_at<CandT>(a, b, j);
-      if (c >= 0 && c < a.vocab) {
-        cand_tok = static_cast<int>(c);
-        cand_x = transform1(f, to_f32<S>(rp[c]), c);
-      }
-    }
+    const CandRec cr = a.cand_rec[row];
     const int mode = row_mode(p, a.vocab);
     float m_x = prev.m, z = prev.z;
     if (prev.flags & kFlagUnscanned) row_stats<TagT>(sh, rp, a.vocab, f, p.temperature, &m_x, &z);
     const Exact ex = exact_support<TagT>(sh, rp, a.vocab, f, p, mode, m_x, z);
     const int n_f = ex.n <= kCap ? collect<TagT>(sh, rp, a.vocab, f, p.temperature, ex.kcut) : 0;
-    write_exact_record(sh, ex, n_f, a.rec_t + row, a.sidx_t + row * kCap, a.sp_t + row * kCap, cand_tok, cand_x,
+    write_exact_record(sh, ex, n_f, a.rec_t + row, a.sidx_t + row * kCap, a.sp_t + row * kCap, cr.tok, cr.x,
                        p.temperature, prev.why);
   }
 }
@@ -1265,7 +1324,7 @@ __global__ __launch_bounds__(kT) void draft_fallback_kernel(Args a) {
   const uint32_t n = *(a.list_cnt + 1);
   for (uint32_t li = blockIdx.x; li < n; li += gridDim.x) {
     const int64_t b = a.list_d[li];
-    if (threadIdx.x == 0) s_len = accept_length<CandT>(a, b, &s_flags);
+    accept_length_block<CandT>(a, b, &s_len, &s_flags);
     __syncthreads();
     const int len = s_len;
     const RowRec prev = a.rec_d[b];
@@ -1395,7 +1454,7 @@ __global__ __launch_bounds__(kT) void resolve_kernel(Args a) {
     atomic_take_u32(a.list_cnt);
     atomic_take_u32(a.list_cnt + 1);
   }
-  if (tid == 0) s_len = accept_length<CandT>(a, b, &s_flags);
+  accept_length_block<CandT>(a, b, &s_len, &s_flags);
   __syncthreads();
   const int len = s_len;
   const int g = a.width - 1;
@@ -1496,15 +1555,17 @@ int pick_slices(int64_t rows, int64_t vocab, int want_wgs, int max_top_k) {
 struct Layout {
   uint64_t counters, scratch;
   uint64_t off_rec_t, off_sidx_t, off_sp_t, off_rec_d, off_sidx_d, off_sp_d, off_pub_t, off_pubs_t, off_pub_d,
-      off_pubs_d, off_list_t, off_list_d;
+      off_pubs_d, off_list_t, off_list_d, off_cand;
   int s_t, s_d;
 };
 
 Layout layout(int64_t batch, int width, int64_t vocab, int max_top_k) {
   Layout l{};
   const int64_t rows = batch * width;
-  l.s_t = pick_slices(rows, vocab, 2048, max_top_k);
-  l.s_d = pick_slices(batch, vocab, 1024, max_top_k);
+  const char* tw = getenv("LS_TUNE_TARGET_WGS");
+  const char* dw = getenv("LS_TUNE_DRAFT_WGS");
+  l.s_t = pick_slices(rows, vocab, tw ? atoi(tw) : 2048, max_top_k);
+  l.s_d = pick_slices(batch, vocab, dw ? atoi(dw) : 1024, max_top_k);
   l.counters = up256(4 * rows) + up256(4 * batch) + 256;
   uint64_t o = 0;
   l.off_rec_t = o; o += up256(sizeof(RowRec) * rows);
@@ -1519,6 +1580,7 @@ Layout layout(int64_t batch, int width, int64_t vocab, int max_top_k) {
   l.off_pubs_d = o; o += up256(16ull * batch * l.s_d);
   l.off_list_t = o; o += up256(4ull * rows);
   l.off_list_d = o; o += up256(4ull * batch);
+  l.off_cand = o; o += up256(sizeof(CandRec) * rows);
   l.scratch = o;
   return l;
 }
@@ -1598,6 +1660,7 @@ extern "C" int ls_verify_sample(const ls_verify_sample_args* in, void* counters,
   a.pubs_d = reinterpret_cast<uint64_t*>(s + l.off_pubs_d);
   a.list_t = reinterpret_cast<int32_t*>(s + l.off_list_t);
   a.list_d = reinterpret_cast<int32_t*>(s + l.off_list_d);
+  a.cand_rec = reinterpret_cast<CandRec*>(s + l.off_cand);
   a.s_t = l.s_t;
   a.s_d = l.s_d;
   a.hint = x.scan_hint;
@@ -1605,7 +1668,8 @@ extern "C" int ls_verify_sample(const ls_verify_sample_args* in, void* counters,
 
   const dim3 g_t(static_cast<unsigned>(rows * l.s_t)), g_d(static_cast<unsigned>(x.batch * l.s_d)),
       g_r(static_cast<unsigned>(x.batch)), g_f(static_cast<unsigned>(rows < 256 ? rows : 256)),
-      g_fd(static_cast<unsigned>(x.batch < 256 ? x.batch : 256));
+      g_fd(static_cast<unsigned>(x.batch < 256 ? x.batch : 256)),
+      g_c(static_cast<unsigned>((rows + rs::kT - 1) / rs::kT));
   void* const* ev = x.timing_events;
 #define LS_EVENT(i)                                                                              \
   do {                                                                                           \
@@ -1620,6 +1684,8 @@ extern "C" int ls_verify_sample(const ls_verify_sample_args* in, void* counters,
     using DS = typename TD::storage;                                                                          \
     const bool tv = tvec_ok && (x.logits_row_stride * sizeof(TS)) % 16 == 0;                                  \
     const bool dv = dvec_ok && (x.draft_stride_b * sizeof(DS)) % 16 == 0 && (x.draft_stride_k * sizeof(DS)) % 16 == 0; \
+    cand_prep_kernel<TT, CT><<<g_c, rs::kT, 0, st>>>(a);                                                      \
+    LS_LAUNCH_CHECK();                                                                                        \
     if (ev) LS_EVENT(0);                                                                                      \
     if (a.hint != kHintExactOnly) {                                                                           \
       if (tv) target_scan_kernel<TT, true, CT, kPathRaw><<<g_t, rs::kT, 0, st>>>(a);                         \
