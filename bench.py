@@ -31,6 +31,17 @@ if ROOT not in sys.path:
 HBM_PEAK_GBS = 8000.0
 V = 151936
 
+# HBM bytes per launch of each workload's dominant kernel, from rocprofv3
+# FETCH_SIZE and WRITE_SIZE passes scaled by the counters' readings for a 1 GiB
+# copy (x2.0 and x1.0).  The commands and raw counter values are in the
+# profiles/ summary named beside each figure.
+TRAFFIC = {
+    "target_scan_kernel": (679_048_173, "profiles/target_scan_kernel_verify_sample_B128_K16_V151936.md"),
+    "greedy_verify_kernel": (622_640_864, "profiles/greedy_verify_kernel_B128_K16_V151936.md"),
+    "window_gather_kernel": (604_246_324, "profiles/window_gather_kernel_B8_L36_Hkv8_D128_ctx131072.md"),
+    "summary_kernel": (646_838_203, "profiles/summary_kernel_B8_L36_R256_W16.md"),
+}
+
 
 def _cpu_model() -> str:
     try:
@@ -330,7 +341,37 @@ class SummaryUpdate:
                           f"median of {n} runs"}
 
 
-WORKLOADS = {w.name: w for w in (GreedyVerify, StochasticVerify, WindowGather, SummaryUpdate)}
+class HbmCopy:
+    """Plain device copy of 1 GiB (torch copy_), the calibration kernel for the
+    FETCH_SIZE / WRITE_SIZE counters: it reads and writes exactly 1 GiB."""
+
+    name = "hbm_copy"
+    metric = "device copy GB/s (read + write) of 1 GiB"
+    unit = "GB/s"
+
+    def __init__(self, dev, nbytes=1 << 30):
+        self.src = torch.empty(nbytes // 2, dtype=torch.bfloat16, device=dev).fill_(1.0)
+        self.dst = torch.empty_like(self.src)
+        self.bytes = 2 * nbytes
+        self.units = self.bytes / 1e9
+        self.kernel = "copy"
+
+    def step(self):
+        self.dst.copy_(self.src)
+
+    def config(self):
+        return {"workload": "torch copy_ of 1 GiB bf16 (counter calibration)", "bytes": self.bytes // 2}
+
+    def cpu_baseline(self, threads):
+        torch.set_num_threads(threads)
+        a = torch.empty(1 << 26, dtype=torch.bfloat16).fill_(1.0)
+        b = torch.empty_like(a)
+        med, n = time_cpu(lambda: b.copy_(a))
+        return {"value": 2 * a.numel() * 2 / med / 1e9, "threads": threads,
+                "sample": f"128 MiB host copy, median of {n} runs"}
+
+
+WORKLOADS = {w.name: w for w in (GreedyVerify, StochasticVerify, WindowGather, SummaryUpdate, HbmCopy)}
 DEFAULT_WORKLOAD = "verify_sample"
 
 
@@ -403,7 +444,8 @@ def main(argv=None):
         "data": "synthetic",
         "config": wl.config(),
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel": wl.kernel,
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": TRAFFIC.get(wl.kernel, (None,))[0],
+                     "traffic_source": TRAFFIC.get(wl.kernel, (None, None))[1], "kernel": wl.kernel,
                      "kernel_avg_us": kernel_ms * 1e3, "algorithmic_bytes": kernel_bytes},
         "step": {"gpu_us": step_gpu_ms * 1e3, "algorithmic_bytes": wl.bytes,
                  "gbs": wl.bytes / (step_gpu_ms / 1e3) / 1e9,
