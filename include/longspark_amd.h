@@ -255,6 +255,46 @@ LS_API int ls_verify_sample(const ls_verify_sample_args* args, void* counters, u
                             void* scratch, uint64_t scratch_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------
+ * Split-engine verification on dense target probabilities.
+ *
+ * ls_decide_acceptance replaces src/longspark/engine/sampling.py:19-35
+ * (decide_acceptance): lengths[b] = number of leading positions j < gamma
+ * with uniforms[b,j] * sampled_q[b,j] < target_probs[b, j, candidates[b,j]]
+ * (strict); target_rows[b, :] = target_probs[b, lengths[b], :] when
+ * target_rows is not NULL.  target_probs rows are contiguous; element strides
+ * are given for the other dimensions.
+ *
+ * ls_finish_sampling replaces src/longspark/engine/sampling.py:38-57
+ * (finish_sampling with uniforms): per request, probs = target_rows[b], or
+ * for a rejected request (b == rejected_rows[r]) the residual
+ * max(target - rejected_q_rows[r], 0) normalised by its mass when the mass
+ * exceeds 1e-8; tokens[b] = #{v : uniforms[b] >= cumsum(probs)[v]}, clamped
+ * to vocab - 1.
+ * ------------------------------------------------------------------------- */
+LS_API int ls_decide_acceptance(const void* candidates, int32_t candidates_dtype, int64_t cand_stride_b,
+                                int64_t cand_stride_k, const float* sampled_q, int64_t q_stride_b,
+                                const float* uniforms, int64_t uniform_stride_b, const float* target_probs,
+                                int64_t probs_stride_b, int64_t probs_stride_k, int64_t batch, int32_t gamma,
+                                int64_t vocab, int64_t* lengths, float* target_rows, int64_t rows_stride_b,
+                                void* stream);
+LS_API int ls_finish_sampling(const float* target_rows, int64_t rows_stride_b, const int64_t* rejected_rows,
+                              int64_t n_rejected, const float* rejected_q_rows, int64_t q_stride_b,
+                              const float* uniforms, int64_t batch, int64_t vocab, int64_t* tokens, void* stream);
+
+/* Fixed-width verify outputs: out_tokens[b, c] = bonus[b] if c == accept_lens[b],
+ * else candidates[b, c+1] (0 in the last column); committed[b] = accept_lens[b] + 1
+ * and next_lengths[b] = prefix_lens[b] + accept_lens[b] + 1 (both may be NULL;
+ * next_lengths has prefix_dtype).  Replaces
+ * SRT/speculative/draft_free_kv_dispatch.py:8-57 (finalize_verify_outputs) and
+ * SRT/speculative/draft_free_kv_utils.py:386-408 (build_greedy_verify_out_tokens). */
+LS_API int ls_finalize_verify_outputs(const void* candidates, int32_t candidates_dtype, int64_t cand_stride_b,
+                                      int64_t cand_stride_k, const void* accept_lens, int32_t lens_dtype,
+                                      int64_t lens_stride, const void* bonus, int32_t bonus_dtype,
+                                      int64_t bonus_stride, const void* prefix_lens, int32_t prefix_dtype,
+                                      int64_t prefix_stride, int64_t batch, int32_t width, int64_t* out_tokens,
+                                      int32_t* committed, void* next_lengths, void* stream);
+
+/* ---------------------------------------------------------------------------
  * Recent-window page tables, window gather and ring append.
  * ------------------------------------------------------------------------- */
 

@@ -93,6 +93,10 @@ _SIGNATURES = {
     "ls_adjust_logits": (I32, [P, I32, I64, I64, I64, I32, P, P, I64, P, I64, P, I32, P, I64, I32, I64, P]),
     "ls_verify_sample_workspace": (I32, [I64, I32, I64, I32, P, P]),
     "ls_verify_sample": (I32, [ctypes.POINTER(VerifySampleArgs), P, U64, P, U64, P]),
+    "ls_decide_acceptance": (I32, [P, I32, I64, I64, P, I64, P, I64, P, I64, I64, I64, I32, I64, P, P, I64, P]),
+    "ls_finish_sampling": (I32, [P, I64, P, I64, P, I64, P, I64, I64, P, P]),
+    "ls_finalize_verify_outputs": (I32, [P, I32, I64, I64, P, I32, I64, P, I32, I64, P, I32, I64, I64, I32, P, P, P,
+                                         P]),
     "ls_raw_page_table": (I32, [P, I64, I64, P, I32, P, I32, I64, I32, P, I64, P, P]),
     "ls_ring_page_table": (I32, [P, I32, P, I32, I64, I32, P, I64, P, P]),
     "ls_kv_window_gather": (I32, [P, P, I32, I32, I64, I64, I32, I32, P, I64, P, I32, I32, P, I32, I64, I32,

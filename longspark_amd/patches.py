@@ -1,0 +1,82 @@
+"""Install these ops in place of the reference implementations.
+
+The reference swaps implementations by module-attribute replacement at
+process start and re-applies it in spawned children
+(src/longspark/patches/__init__.py:15-33, src/longspark/patches/gqa5_attention.py:109-112).
+``install()`` does the same for the hot-path call sites: every target module
+that is importable in this process gets its attributes replaced; modules that
+are absent are skipped and reported.  Call it at process start and in the
+entry point of every spawned worker, before the first verify step.
+
+``SRT`` = ``sglang.srt``.
+"""
+
+from __future__ import annotations
+
+import importlib
+from typing import Dict, Iterable, List, Optional, Tuple
+
+
+def replacements() -> Dict[str, Dict[str, object]]:
+    """module name -> {attribute: replacement}, for every hot-path call site."""
+    from . import kvwindow, penalties, summary, verify
+
+    return {
+        # greedy verify (SPEC/dspark_components/kernels/accept_greedy.py:22-60)
+        "sglang.srt.speculative.dspark_components.kernels.accept_greedy": {"AcceptGreedy": verify.AcceptGreedy},
+        # split-engine two-phase rejection sampling (src/longspark/engine/sampling.py:19-57)
+        "longspark.engine.sampling": {"decide_acceptance": verify.decide_acceptance,
+                                      "finish_sampling": verify.finish_sampling},
+        # fixed-width verify outputs (SPEC/draft_free_kv_utils.py:386-408,
+        # SPEC/draft_free_kv_dispatch.py:32-57)
+        "sglang.srt.speculative.draft_free_kv_utils": {
+            "build_greedy_verify_out_tokens": verify.build_greedy_verify_out_tokens},
+        "sglang.srt.speculative.draft_free_kv_dispatch": {"finalize_verify_outputs": verify.finalize_verify_outputs},
+        # vocabulary bitmask (SRT/constrained/triton_ops/bitmask_ops.py:84-141)
+        "sglang.srt.constrained.triton_ops.bitmask_ops": {
+            "apply_token_bitmask_inplace_triton": penalties.apply_token_bitmask_inplace},
+        # summary state (SPEC/global16_raw256_incremental.py:400-584; the GQA-5
+        # adapter's wrappers are covered by the same functions)
+        "sglang.srt.speculative.global16_raw256_incremental": {
+            "cache_position_scores": summary.cache_position_scores,
+            "merge_accepted_positions_": summary.merge_accepted_positions_},
+        # recent window (SPEC/global16_raw256_draft_fused.py:372-413, engine/draft.py:14-21)
+        "sglang.srt.speculative.global16_raw256_draft_fused": {
+            "build_raw256_page_table": kvwindow.build_raw256_page_table},
+        "longspark.engine.draft": {"ring_page_table": kvwindow.ring_page_table},
+        "longspark.engine.state_export": {"gather_selected_kv": _gather_selected_kv_pool},
+    }
+
+
+def _gather_selected_kv_pool(pool, layer_ids, locations, *, tp, rank, group, workspace):
+    """Signature of src/longspark/engine/state_export.py:14 (``pool.get_kv_buffer(layer)``
+    per layer); one rank only -- a tensor-parallel export keeps the reference path."""
+    if tp != 1:
+        raise ValueError("gather_selected_kv replacement covers the single-rank export only")
+    from . import kvwindow
+
+    if not layer_ids or locations.ndim != 1 or locations.numel() == 0:
+        raise ValueError("KV export requires selected layers and nonempty 1D locations")
+    keys, values = zip(*(pool.get_kv_buffer(layer) for layer in layer_ids))
+    return kvwindow.gather_selected_kv(list(keys), list(values), locations)
+
+
+def install(modules: Optional[Iterable[str]] = None) -> Tuple[List[str], List[str]]:
+    """Replace the attributes of every importable target module.
+
+    Returns (patched module names, skipped module names).  ``modules`` limits
+    the install to the given names.
+    """
+    table = replacements()
+    names = list(table) if modules is None else list(modules)
+    patched, skipped = [], []
+    for name in names:
+        try:
+            mod = importlib.import_module(name)
+        except ImportError:
+            skipped.append(name)
+            continue
+        for attr, fn in table[name].items():
+            setattr(mod, attr, fn)
+        patched.append(name)
+    return patched, skipped

@@ -9,6 +9,7 @@ synchronising the host.
 
 from __future__ import annotations
 
+from dataclasses import dataclass
 from typing import Optional
 
 import torch
@@ -118,6 +119,128 @@ def compute_greedy_accept_len_and_bonus_from_logits(*, candidates, target_logits
     accept, bonus, _ = verify_greedy(logits=target_logits, candidates=candidates, width=draft_token_num,
                                      cand_first_col=1)
     return accept, bonus
+
+
+# --------------------------------------------------------------------------
+# split-engine two-phase rejection sampling (dense target probabilities)
+# --------------------------------------------------------------------------
+
+@dataclass
+class AcceptanceDecision:
+    """Same fields as src/longspark/engine/sampling.py:11-16."""
+    lengths: torch.Tensor
+    rejected_rows: torch.Tensor
+    rejection_positions: torch.Tensor
+    target_rows: torch.Tensor
+
+
+def decide_acceptance(*, candidates, sampled_q, target_probs, uniforms) -> AcceptanceDecision:
+    """src/longspark/engine/sampling.py:19-35 on the GPU.
+
+    ``candidates`` ``[B, gamma]`` drafted tokens, ``sampled_q`` / ``uniforms``
+    ``[B, gamma]`` fp32, ``target_probs`` ``[B, gamma+1, V]`` fp32.  The
+    accepted lengths and the target row at each length come from one kernel;
+    ``rejected_rows`` (a data-dependent size) is selected with torch from the
+    lengths, as the reference does.
+    """
+    what = "decide_acceptance"
+    batch, gamma = candidates.shape
+    if sampled_q.shape != (batch, gamma) or uniforms.shape != (batch, gamma):
+        raise ValueError("sampled q and uniforms must match the seven proposal positions")
+    if target_probs.shape[:2] != (batch, gamma + 1):
+        raise ValueError("target must verify proposal width plus one bonus row")
+    dev = _lib.require_cuda(candidates, sampled_q, target_probs, uniforms, what=what)
+    if target_probs.dtype != torch.float32 or sampled_q.dtype != torch.float32 or uniforms.dtype != torch.float32:
+        raise ValueError(f"{what}: probabilities, q and uniforms must be fp32")
+    if target_probs.stride(2) != 1 or sampled_q.stride(1) != 1 or uniforms.stride(1) != 1:
+        raise ValueError(f"{what}: the last dimension must be contiguous")
+    vocab = target_probs.shape[2]
+    lengths = torch.empty(batch, dtype=torch.int64, device=dev)
+    rows = torch.empty(batch, vocab, dtype=torch.float32, device=dev)
+    _lib.call("ls_decide_acceptance", candidates.data_ptr(), _lib.dtype_code(candidates), candidates.stride(0),
+              candidates.stride(1), sampled_q.data_ptr(), sampled_q.stride(0), uniforms.data_ptr(),
+              uniforms.stride(0), target_probs.data_ptr(), target_probs.stride(0), target_probs.stride(1), batch,
+              gamma, vocab, lengths.data_ptr(), rows.data_ptr(), rows.stride(0), _lib.stream_of(dev))
+    rejected = torch.arange(batch, device=dev)[lengths < gamma]
+    return AcceptanceDecision(lengths=lengths, rejected_rows=rejected, rejection_positions=lengths[rejected],
+                              target_rows=rows)
+
+
+def finish_sampling(decision: AcceptanceDecision, rejected_q_rows, *, generator=None, uniforms=None):
+    """src/longspark/engine/sampling.py:38-57 on the GPU.
+
+    With ``uniforms`` the token is ``#{v : u >= CDF(v)}`` of the request's
+    distribution (the normalised residual for rejected requests), clamped to
+    V-1.  Without them, one uniform per request is drawn from ``generator``
+    on the device and used the same way, which samples the same distribution
+    as the reference's ``torch.multinomial``.
+    """
+    what = "finish_sampling"
+    target = decision.target_rows
+    expected = (decision.rejected_rows.numel(), target.shape[-1])
+    if rejected_q_rows.shape != expected:
+        raise ValueError(f"expected rejected q shape {expected}, got {rejected_q_rows.shape}")
+    batch, vocab = target.shape
+    dev = _lib.require_cuda(target, rejected_q_rows, decision.rejected_rows, uniforms, what=what)
+    if uniforms is None:
+        uniforms = torch.rand(batch, generator=generator, device=dev)
+    if uniforms.shape != (batch,):
+        raise ValueError("one final uniform is required per request")
+    if target.dtype != torch.float32 or rejected_q_rows.dtype != torch.float32:
+        raise ValueError(f"{what}: target rows and q rows must be fp32")
+    if target.stride(1) != 1 or (rejected_q_rows.numel() and rejected_q_rows.stride(1) != 1):
+        raise ValueError(f"{what}: rows must be contiguous")
+    rej = decision.rejected_rows.to(torch.int64).contiguous()
+    uniforms = uniforms.to(torch.float32).contiguous()
+    out = torch.empty(batch, dtype=torch.int64, device=dev)
+    _lib.call("ls_finish_sampling", target.data_ptr(), target.stride(0), rej.data_ptr(), rej.numel(),
+              rejected_q_rows.data_ptr(), rejected_q_rows.stride(0) if rejected_q_rows.numel() else 0,
+              uniforms.data_ptr(), batch, vocab, out.data_ptr(), _lib.stream_of(dev))
+    return out
+
+
+# --------------------------------------------------------------------------
+# fixed-width verify outputs
+# --------------------------------------------------------------------------
+
+def _finalize(candidates, accept_lens, bonus, prefix_lens, what, with_counts):
+    if candidates.ndim != 2 or candidates.shape[1] < 2:
+        raise ValueError("verification candidates must have shape [batch, width>=2]")
+    batch, width = candidates.shape
+    named = [("accept_lens", accept_lens), ("bonus", bonus)] + ([("prefix_lens", prefix_lens)] if with_counts else [])
+    for name, value in named:
+        if value.shape != (batch,) or value.device != candidates.device:
+            raise ValueError(f"{name} must have one device row per request")
+        if value.dtype not in (torch.int32, torch.int64):
+            raise ValueError(f"{name} must have an integer dtype")
+    dev = _lib.require_cuda(candidates, accept_lens, bonus, prefix_lens, what=what)
+    out = torch.empty((batch, width), device=dev, dtype=torch.int64)
+    committed = next_lengths = None
+    if with_counts:
+        committed = torch.empty((batch,), device=dev, dtype=torch.int32)
+        next_lengths = torch.empty((batch,), device=prefix_lens.device, dtype=prefix_lens.dtype)
+    _lib.call("ls_finalize_verify_outputs", candidates.data_ptr(), _lib.dtype_code(candidates), candidates.stride(0),
+              candidates.stride(1), accept_lens.data_ptr(), _lib.dtype_code(accept_lens), accept_lens.stride(0),
+              bonus.data_ptr(), _lib.dtype_code(bonus), bonus.stride(0),
+              _lib.ptr(prefix_lens), _lib.dtype_code(prefix_lens) if with_counts else _lib.LS_I64,
+              prefix_lens.stride(0) if with_counts else 0, batch, width, out.data_ptr(), _lib.ptr(committed),
+              _lib.ptr(next_lengths), _lib.stream_of(dev))
+    return out, committed, next_lengths
+
+
+def finalize_verify_outputs(*, candidates, accept_lens, bonus, prefix_lens):
+    """SRT/speculative/draft_free_kv_dispatch.py:32-57: ``(out_tokens i64 [B, W],
+    committed i32 [B], next_lengths [B])``; fresh tensors, as the scheduler may keep them."""
+    return _finalize(candidates, accept_lens, bonus, prefix_lens, "finalize_verify_outputs", True)
+
+
+def build_greedy_verify_out_tokens(*, candidates, accept_lens, bonus):
+    """SRT/speculative/draft_free_kv_utils.py:386-408: the ``[B, W]`` int64 committed-token buffer."""
+    if candidates.ndim != 2 or accept_lens.shape != (candidates.shape[0],):
+        raise ValueError("DRAFT_FREE_KV verify tensors have incompatible shapes")
+    if bonus.shape != (candidates.shape[0],):
+        raise ValueError("DRAFT_FREE_KV bonus must have one token per request")
+    return _finalize(candidates, accept_lens, bonus, None, "build_greedy_verify_out_tokens", False)[0]
 
 
 # --------------------------------------------------------------------------

@@ -114,6 +114,19 @@ def finish_sampling(decision: AcceptanceDecision, rejected_q_rows, uniforms):
     return (uniforms[:, None] >= probs.cumsum(-1)).sum(-1).clamp_max(probs.shape[-1] - 1)
 
 
+def finalize_verify_outputs(candidates, accept_lens, bonus, prefix_lens):
+    """SPEC/draft_free_kv_dispatch.py:8-57 restated: ``out[b, c]`` is the bonus at
+    ``c == L_b``, else ``candidates[b, c+1]`` (0 in the last column);
+    ``committed = L + 1``; ``next = prefix + L + 1``."""
+    batch, width = candidates.shape
+    out = torch.zeros(batch, width, dtype=torch.int64)
+    out[:, :-1] = candidates[:, 1:].to(torch.int64)
+    out[torch.arange(batch), accept_lens.long()] = bonus.to(torch.int64)
+    committed = (accept_lens.to(torch.int64) + 1).to(torch.int32)
+    next_lengths = (prefix_lens.to(torch.int64) + accept_lens.to(torch.int64) + 1).to(prefix_lens.dtype)
+    return out, committed, next_lengths
+
+
 # --------------------------------------------------------------------------
 # temperature softmax and inverse-CDF sampling
 # --------------------------------------------------------------------------

@@ -185,3 +185,12 @@ def test_chain_sampling_matches_single_q_when_q_is_dense_softmax():
     chain_bonus = preds[aidx[torch.arange(b), anum.long()].long()].long()
     # identical except where the residual mass is degenerate (not here) or a CDF tie
     assert (chain_bonus == bonus).float().mean() > 0.9
+
+
+def test_finalize_outputs_hand_case():
+    cand = torch.tensor([[5, 11, 12, 13], [7, 21, 22, 23]])
+    out, committed, nxt = ov.finalize_verify_outputs(cand, torch.tensor([1, 3], dtype=torch.int32),
+                                                     torch.tensor([99, 98]), torch.tensor([100, 200]))
+    # request 0 accepts one draft (11), bonus at column 1; request 1 accepts all three
+    assert out.tolist() == [[11, 99, 13, 0], [21, 22, 23, 98]]
+    assert committed.tolist() == [2, 4] and nxt.tolist() == [102, 204]
