@@ -96,6 +96,8 @@ struct Args {
   uint64_t* pubs_d;   // [B, S_d, 2]
   struct CandRec* cand_rec;  // [B*K] transformed logit of each row's drafted token
   int hint;            // which scan kernels the launcher runs (Hint)
+  int wave;            // 1: target_wave_kernel runs (takes raw rows with k <= kWaveMaxK)
+  int wave_only;       // 1: no workgroup raw scan follows (the wave kernel lists every other raw row)
   uint32_t* list_cnt;  // counters [2]: rows waiting for the exact fallback (target, draft)
   int32_t* list_t;     // [B*K]
   int32_t* list_d;     // [B]
@@ -1073,18 +1075,20 @@ __device__ __forceinline__ int slices_clamped(int s, int64_t vocab) { return s; 
 // kernel alone).  With the raw kernel alone (hint), an ineligible row is
 // handed to the exact fallback unscanned.
 enum Path : int { kPathRaw = 0, kPathExact = 1 };
+constexpr int kWaveMaxRowK = kWave;  // top-k rows the one-wave kernel takes (k <= 64)
 enum Hint : int { kHintBoth = 0, kHintRawOnly = 1, kHintExactOnly = 2 };
 
 template <typename Tag, bool kVec, int kPath>
 __device__ void process_row(Shared& sh, const typename Tag::storage* row, int64_t vocab, const Params& p,
                             const XForm& f, int slices, int slice, uint64_t* pub, uint64_t* pubs, uint32_t* cnt,
                             RowRec* rec, int32_t* sidx, float* sp, int cand_tok, float cand_x, uint32_t* list_cnt,
-                            int32_t* list, int32_t list_id, bool raw_ok, int hint) {
+                            int32_t* list, int32_t list_id, bool raw_ok, int hint, int wave) {
   const int mode = row_mode(p, vocab);
   const bool raw = mode == kModeTopK && raw_ok;
   if constexpr (kPath == kPathRaw) {
+    if (wave && raw && p.top_k <= kWaveMaxRowK) return;  // scanned by the one-wave kernel
     if (!raw) {
-      if (hint == kHintRawOnly && slice == 0 && threadIdx.x == 0) {
+      if (hint == kHintRawOnly && !wave && slice == 0 && threadIdx.x == 0) {
         RowRec rr{};
         rr.flags = kFlagOverflow | kFlagUnscanned;
         rr.why = kWhyHint;
@@ -1158,6 +1162,494 @@ __global__ __launch_bounds__(kT) void cand_prep_kernel(Args a) {
   a.cand_rec[row] = cr;
 }
 
+// ------------------------------------------- one wavefront per target row ---
+//
+// Top-k rows eligible for the raw-logit filter with k <= kWaveMaxK are
+// scanned by a single wavefront each, so a row needs no workgroup barrier
+// and one row's selection and finalisation overlap other rows' streaming on
+// the same CU.  Every row of a batch is resident at once (2048 rows = 8
+// waves per CU).  Each lane keeps kWaveDepth 16-byte loads in flight (16 KB
+// per wave); the candidate buffer, its radix-select histogram and the
+// support sort live in the wave's own LDS.  Semantics are those of the
+// workgroup raw path: raw values are filtered against a threshold that only
+// rises, candidates are transformed when the buffer is compacted and at the
+// end, and the support is cut by top-k (ties to the lowest index), top-p and
+// min-p.
+
+constexpr int kWaveBuf = 2304;                    // candidate entries per wave (19 KB of LDS with the histogram: at most 8 waves per CU, so 2048 rows spread evenly)
+constexpr int kWaveDepth = 16;                    // 16-byte loads in flight per lane
+constexpr int kWaveMaxK = kWaveMaxRowK;           // prologue threshold from 64 lane maxima
+constexpr int kWaveTrigger = kWaveBuf - kWave * 8;  // room for one step of appends
+
+struct WaveShared {
+  uint64_t buf[kWaveBuf];
+  uint32_t hist[256];
+};
+
+// Orders the wave's own LDS accesses (no instruction on gfx950: a wave's LDS
+// operations complete in order); keeps the compiler from moving them across.
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ __forceinline__ int wave_excl_scan(int v, int* total) {
+  const int lane = threadIdx.x & (kWave - 1);
+  int inc = v;
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const int t = __shfl_up(inc, o, kWave);
+    if (lane >= o) inc += t;
+  }
+  *total = __shfl(inc, kWave - 1, kWave);
+  return inc - v;
+}
+
+__device__ __forceinline__ float wave_incl_scan_f(float v) {
+  const int lane = threadIdx.x & (kWave - 1);
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const float t = __shfl_up(v, o, kWave);
+    if (lane >= o) v += t;
+  }
+  return v;
+}
+
+// Append the raw elements x[0..P) >= tau (all lanes call; count is uniform):
+// one ballot per element position and the lane's rank among the passing
+// lanes from mbcnt, so no cross-lane permute sits on the path.
+template <int P>
+__device__ __forceinline__ void wave_append(WaveShared& ws, int& count, const float* x, float tau, int64_t e0) {
+#pragma unroll
+  for (int q = 0; q < P; ++q) {
+    const bool pass = x[q] >= tau;
+    const uint64_t m = __ballot(pass);
+    if (m) {
+      if (pass) {
+        const int pos = count + __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
+                                                          __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u));
+        if (pos < kWaveBuf) ws.buf[pos] = cand_key(x[q], static_cast<int>(e0 + q));
+      }
+      count += __popcll(m);
+    }
+  }
+}
+
+__device__ __forceinline__ void wave_transform(WaveShared& ws, const XForm& f, int from, int to) {
+  if (!(f.pbits || f.mbits)) return;
+  to = min(to, kWaveBuf);
+  for (int i = from + static_cast<int>(threadIdx.x & (kWave - 1)); i < to; i += kWave) {
+    const uint64_t key = ws.buf[i];
+    const int idx = key_idx(key);
+    ws.buf[i] = cand_key(transform1(f, key_s(key), idx), idx);
+  }
+  wave_sync();
+}
+
+// Ordered-s of the k-th largest of buf[0..n) (ties counted), 1 <= k <= n,
+// by an MSB-first radix select over 8-bit digits.  With bf16_keys every key
+// holds a bf16 value, whose ordered form has its low 16 bits all 0 (positive)
+// or all 1 (negative): two passes then fix the whole value.
+__device__ uint32_t wave_select_kth(WaveShared& ws, int n, int k, bool bf16_keys = false) {
+  const int lane = threadIdx.x & (kWave - 1);
+  uint32_t prefix = 0, pmask = 0;
+  int remaining = k;
+  const int passes = bf16_keys ? 2 : 4;
+  for (int pass = 0; pass < passes; ++pass) {
+    const int shift = 24 - 8 * pass;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) ws.hist[4 * lane + j] = 0;
+    wave_sync();
+    for (int i = lane; i < n; i += kWave) {
+      const uint32_t h = static_cast<uint32_t>(ws.buf[i] >> 32);
+      if ((h & pmask) == prefix) atomicAdd(&ws.hist[(h >> shift) & 255u], 1u);
+    }
+    wave_sync();
+    uint32_t c[4], local = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      c[j] = ws.hist[4 * lane + j];
+      local += c[j];
+    }
+    uint32_t suf = local;  // inclusive suffix sum: lanes above own larger digits
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+      const uint32_t v = __shfl_down(suf, o, kWave);
+      if (lane + o < kWave) suf += v;
+    }
+    uint32_t above = suf - local;
+    int sel = -1, sel_above = 0;
+#pragma unroll
+    for (int j = 3; j >= 0; --j) {
+      if (above < static_cast<uint32_t>(remaining) && above + c[j] >= static_cast<uint32_t>(remaining)) {
+        sel = 4 * lane + j;
+        sel_above = static_cast<int>(above);
+      }
+      above += c[j];
+    }
+    const uint64_t who = __ballot(sel >= 0);
+    const int src = __ffsll(static_cast<long long>(who)) - 1;
+    const uint32_t d = static_cast<uint32_t>(__shfl(sel, src, kWave));
+    remaining -= __shfl(sel_above, src, kWave);
+    prefix |= d << shift;
+    pmask |= 255u << shift;
+    wave_sync();
+  }
+  if (bf16_keys) prefix |= (prefix & 0x80000000u) ? 0u : 0xFFFFu;
+  return prefix;
+}
+
+// Keep entries of buf[0..n) whose ordered-s is >= thr (stable); returns the count.
+__device__ int wave_compact_ge(WaveShared& ws, int n, uint32_t thr) {
+  const int lane = threadIdx.x & (kWave - 1);
+  int out = 0;
+  for (int r = 0; r < n; r += kWave) {
+    const int i = r + lane;
+    const uint64_t key = i < n ? ws.buf[i] : 0;
+    const bool keep = i < n && static_cast<uint32_t>(key >> 32) >= thr;
+    const uint64_t m = __ballot(keep);
+    const int off = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
+                                              __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u));
+    wave_sync();
+    if (keep) ws.buf[out + off] = key;  // out + off <= i: never ahead of an unread entry
+    out += __popcll(m);
+  }
+  wave_sync();
+  return out;
+}
+
+// Sort buf[0..n) descending (bitonic, zero-padded to a power of two).
+__device__ void wave_sort_desc(WaveShared& ws, int n) {
+  const int lane = threadIdx.x & (kWave - 1);
+  int np = 2;
+  while (np < n) np <<= 1;
+  for (int i = n + lane; i < np; i += kWave) ws.buf[i] = 0;
+  wave_sync();
+  for (int size = 2; size <= np; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int i = lane; i < np / 2; i += kWave) {
+        const int lo = 2 * i - (i & (stride - 1));
+        const int hi = lo + stride;
+        const bool desc = (lo & size) == 0;
+        const uint64_t a = ws.buf[lo], b = ws.buf[hi];
+        if ((a < b) == desc) {
+          ws.buf[lo] = b;
+          ws.buf[hi] = a;
+        }
+      }
+      wave_sync();
+    }
+  }
+}
+
+// Transform what is pending, then keep the k largest (within the rounding
+// margin); returns the new raw threshold (or -FLT_MAX if n <= k).
+__device__ __forceinline__ float wave_compact_topk(WaveShared& ws, const XForm& f, int& count, int& ntrans, int k,
+                                                  bool bf16_raw) {
+  wave_transform(ws, f, ntrans, count);
+  ntrans = count;
+  if (count <= k) return -FLT_MAX;
+  // penalties change values; the mask only sets -inf (a bf16 value)
+  const float xk = unordered_f32(wave_select_kth(ws, count, k, bf16_raw && !f.pbits));
+  const float thr = x_lower(xk);
+  count = wave_compact_ge(ws, count, ordered_f32(thr));
+  ntrans = count;
+  return thr;
+}
+
+template <typename TagT, typename CandT>
+__global__ __launch_bounds__(kWave) void target_wave_kernel(Args a) {
+  __shared__ WaveShared ws;
+  using S = typename TagT::storage;
+  constexpr int P = TagT::kPerVec;
+  const int64_t row = blockIdx.x;
+  const int64_t b = row / a.width;
+  const int lane = threadIdx.x;
+  const S* rp = static_cast<const S*>(a.logits) + row * a.lrs;
+  const uint4* vp = reinterpret_cast<const uint4*>(rp);
+  const int64_t nfull = a.vocab / P;               // whole 16-byte vectors
+  const int64_t steps = (nfull + kWave - 1) / kWave;
+  const int64_t last = nfull - 1;
+  // The first chunk is requested before the row's parameters are read, so
+  // its latency overlaps the set-up (a row of another path discards it).
+  uint4 r[kWaveDepth], q[kWaveDepth];
+#pragma unroll
+  for (int u = 0; u < kWaveDepth; ++u) r[u] = load16_stream(vp + min<int64_t>(u * kWave + lane, last));
+#pragma unroll
+  for (int u = 0; u < kWaveDepth; ++u) q[u] = load16_stream(vp + min<int64_t>((kWaveDepth + u) * kWave + lane, last));
+  Params p{a.temps[b], a.top_ks ? max(a.top_ks[b], 1) : static_cast<int>(a.vocab), a.top_ps ? a.top_ps[b] : 1.f,
+           a.min_ps ? a.min_ps[b] : 0.f};
+  const XForm f = target_xform(a, b, row);
+  const int mode = row_mode(p, a.vocab);
+  const bool raw = mode == kModeTopK && raw_filter_ok(f, a.pnonpos, b);
+  if (!(raw && p.top_k <= kWaveMaxK)) {
+    // Rows of the other paths.  In a raw-only launch the rows that are not raw
+    // go to the exact fallback unscanned; raw rows with larger k go there too
+    // when no workgroup raw scan follows.
+    if (((!raw && a.hint == kHintRawOnly) || (raw && a.wave_only)) && lane == 0) {
+      RowRec rr{};
+      rr.flags = kFlagOverflow | kFlagUnscanned;
+      rr.why = kWhyHint;
+      a.rec_t[row] = rr;
+      a.list_t[atomic_add_u32(a.list_cnt, 1u)] = static_cast<int32_t>(row);
+    }
+    return;
+  }
+  const int k = p.top_k;
+  constexpr bool kBf16 = sizeof(S) == 2 && TagT::kPerVec == 8 && !__is_same(TagT, F16);
+  const CandRec cr = a.cand_rec[row];
+  // Chunks of kWaveDepth steps: every chunk's loads are issued together and
+  // consumed in order, so no load stays in flight across the loop's back edge
+  // (a loop-carried register with a pending load makes the compiler drain all
+  // loads, or copy the register, at every iteration).
+
+  float tau = -FLT_MAX;
+  if (steps >= kWaveDepth) {
+    // Prologue threshold: the k-th largest of the 64 lane maxima over the
+    // first kWaveDepth vectors of each lane, counting only elements the
+    // transform leaves unchanged (bit clear in the penalty bitmap, set in the
+    // mask), is a transformed value of k distinct elements: a lower bound of
+    // the row's k-th largest.
+    // Each lane keeps its 4 largest unchanged elements; the k-th largest of
+    // those 256 values (ties counted) bounds the row's k-th largest from below.
+    // The penalty and mask words are fetched 16 vectors at a time.
+    float t0 = -INFINITY, t1 = -INFINITY, t2 = -INFINITY, t3 = -INFINITY;
+    constexpr int kHalf = 16;
+#pragma unroll
+    for (int h = 0; h < kWaveDepth / kHalf; ++h) {
+      uint32_t pw[kHalf], mw[kHalf];
+#pragma unroll
+      for (int u = 0; u < kHalf; ++u) {
+        pw[u] = 0u;
+        mw[u] = ~0u;
+      }
+      if (f.pbits) {
+#pragma unroll
+        for (int u = 0; u < kHalf; ++u)
+          pw[u] = f.pbits[(static_cast<int64_t>((h * kHalf + u) * kWave + lane) * P) >> 5];
+      }
+      if (f.mbits) {
+#pragma unroll
+        for (int u = 0; u < kHalf; ++u)
+          mw[u] = f.mbits[(static_cast<int64_t>((h * kHalf + u) * kWave + lane) * P) >> 5];
+      }
+#pragma unroll
+      for (int u = 0; u < kHalf; ++u) {
+        float x[P];
+        unpack16<TagT>(r[h * kHalf + u], x);
+        const int sh = static_cast<int>((static_cast<int64_t>((h * kHalf + u) * kWave + lane) * P) & 31);
+        const uint32_t ok = (~pw[u] & mw[u]) >> sh;
+#pragma unroll
+        for (int qq = 0; qq < P; ++qq) {
+          // branch-free insertion into the sorted top 4 (t0 >= t1 >= t2 >= t3):
+          // each new rank is the median of its old value, the one above and v
+          const float v = ((ok >> qq) & 1u) ? x[qq] : -INFINITY;
+          t3 = __builtin_amdgcn_fmed3f(t2, t3, v);
+          t2 = __builtin_amdgcn_fmed3f(t1, t2, v);
+          t1 = __builtin_amdgcn_fmed3f(t0, t1, v);
+          t0 = fmaxf(t0, v);
+        }
+      }
+    }
+    ws.buf[4 * lane + 0] = cand_key(t0, 0);
+    ws.buf[4 * lane + 1] = cand_key(t1, 0);
+    ws.buf[4 * lane + 2] = cand_key(t2, 0);
+    ws.buf[4 * lane + 3] = cand_key(t3, 0);
+    wave_sync();
+    const float tk = unordered_f32(wave_select_kth(ws, 4 * kWave, k));
+    if (tk > -INFINITY) tau = x_lower(tk);
+  }
+
+  int count = 0, ntrans = 0, ovf = 0;
+  float raw_max = -INFINITY;
+  // One step consumes ring slot u (vector st*64 + lane) and refills it with
+  // the vector kWaveDepth steps ahead.  Slots are fixed registers and refills
+  // are unconditional (clamped to the last vector past the end), so no copy
+  // or branch makes the compiler wait for younger loads than the slot's own.
+  auto step = [&](float* x, int64_t st) __attribute__((always_inline)) {
+    const int64_t idx = st * kWave + lane;
+    if (idx >= nfull) {
+#pragma unroll
+      for (int q = 0; q < P; ++q) x[q] = -INFINITY;
+    }
+    float vmax = x[0];
+#pragma unroll
+    for (int q = 1; q < P; ++q) vmax = fmaxf(vmax, x[q]);
+    raw_max = fmaxf(raw_max, vmax);
+    // Appends past the buffer are dropped and counted; the chunk boundary
+    // turns that into an overflow (the row is resolved by the exact fallback).
+    if (__ballot(vmax >= tau)) wave_append<P>(ws, count, x, tau, idx * P);
+  };
+  // Two chunk buffers: while one chunk is consumed the next one is in flight.
+  // Refills are unconditional (clamped to the last vector past the end) so
+  // the buffers need no merge copies; the loop is unrolled by two so each
+  // buffer keeps its registers.  Between chunks, compact once the buffer
+  // holds more than 2k entries, so the threshold follows the running k-th
+  // largest and few elements arrive.
+  const int soft = max(2 * k, 64);
+#define LS_WAVE_BOUNDARY()                                                 \
+  do {                                                                      \
+    if (count > kWaveBuf && !ovf) {                                         \
+      ovf = kWhyLost;                                                       \
+      tau = INFINITY;                                                       \
+    } else if (count > soft && !ovf) {                                      \
+      wave_sync();                                                          \
+      tau = fmaxf(tau, wave_compact_topk(ws, f, count, ntrans, k, kBf16));         \
+      if (count > kWaveTrigger) { ovf = kWhyTies; tau = INFINITY; }         \
+    }                                                                       \
+  } while (0)
+#define LS_WAVE_CONSUME(BUF, S0)                                            \
+  do {                                                                      \
+    _Pragma("unroll") for (int u = 0; u < kWaveDepth; ++u) {                \
+      if ((S0) + u < steps) {                                               \
+        float x[P];                                                         \
+        unpack16<TagT>(BUF[u], x);                                          \
+        step(x, (S0) + u);                                                  \
+      }                                                                     \
+    }                                                                       \
+  } while (0)
+#define LS_WAVE_ISSUE(BUF, S0)                                              \
+  do {                                                                      \
+    _Pragma("unroll") for (int u = 0; u < kWaveDepth; ++u)                  \
+      BUF[u] = load16_stream(vp + min<int64_t>(((S0) + u) * kWave + lane, last)); \
+  } while (0)
+  LS_WAVE_CONSUME(r, 0);  // chunk 0 (read by the prologue); chunk 1 is in q
+  for (int64_t s0 = kWaveDepth; s0 < steps; s0 += 2 * kWaveDepth) {
+    LS_WAVE_ISSUE(r, s0 + kWaveDepth);
+    LS_WAVE_BOUNDARY();
+    LS_WAVE_CONSUME(q, s0);
+    if (s0 + kWaveDepth >= steps) break;
+    LS_WAVE_ISSUE(q, s0 + 2 * kWaveDepth);
+    LS_WAVE_BOUNDARY();
+    LS_WAVE_CONSUME(r, s0 + kWaveDepth);
+  }
+#undef LS_WAVE_ISSUE
+#undef LS_WAVE_CONSUME
+#undef LS_WAVE_BOUNDARY
+  // Elements past the last whole vector (vocab not a multiple of P).
+  {
+    const int64_t v = nfull * P + lane;
+    float x[1] = {v < a.vocab ? to_f32<S>(rp[v]) : -INFINITY};
+    raw_max = fmaxf(raw_max, x[0]);
+    if (__ballot(x[0] >= tau)) wave_append<1>(ws, count, x, tau, v);
+  }
+  raw_max = wave_max(raw_max);
+  if (count > kWaveBuf) ovf |= kWhyLost;
+  wave_sync();
+
+  // Final support: keep the k largest transformed values, re-key by x / T.
+  const float t = p.temperature;
+  if (!ovf) {
+    wave_compact_topk(ws, f, count, ntrans, k, kBf16);
+    for (int i = lane; i < count; i += kWave) {
+      const uint64_t key = ws.buf[i];
+      ws.buf[i] = cand_key(key_s(key) / t, key_idx(key));
+    }
+    wave_sync();
+  }
+  int n = count;
+  float m = 0.f, zf = 0.f;
+  int n_f = 0;
+  if (!ovf) {
+    if (n <= kWave) {
+      // one key per lane: bitonic sort across the wave, descending
+      uint64_t key = lane < n ? ws.buf[lane] : 0;
+#pragma unroll
+      for (int size = 2; size <= kWave; size <<= 1) {
+#pragma unroll
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+          const uint64_t o = __shfl_xor(key, stride, kWave);
+          const bool desc = (lane & size) == 0 || size == kWave;
+          const bool lower = (lane & stride) == 0;
+          key = (lower == desc) ? (key > o ? key : o) : (key < o ? key : o);
+        }
+      }
+      wave_sync();
+      ws.buf[lane] = key;
+      wave_sync();
+    } else {
+      wave_sort_desc(ws, n);
+    }
+    if (n > k) n = k;
+    m = n > 0 ? key_s(ws.buf[0]) : -INFINITY;
+    float acc = 0.f;
+    for (int i = lane; i < n; i += kWave) acc += __expf(key_s(ws.buf[i]) - m);
+    const float z1 = wave_sum(acc);
+    n_f = n;
+    if (p.top_p < 1.0f && n > 0) {
+      // first entry whose exclusive prefix of probabilities exceeds top_p
+      float carry = 0.f;
+      for (int r0 = 0; r0 < n; r0 += kWave) {
+        const int i = r0 + lane;
+        const float pi = i < n ? __expf(key_s(ws.buf[i]) - m) / z1 : 0.f;
+        const float inc = wave_incl_scan_f(pi);
+        const uint64_t hit = __ballot(i < n && carry + inc - pi > p.top_p);
+        if (hit) {
+          n_f = r0 + __ffsll(static_cast<long long>(hit)) - 1;
+          break;
+        }
+        carry += __shfl(inc, kWave - 1, kWave);
+      }
+    }
+    if (p.min_p > 0.f && n_f > 0) {
+      float a2 = 0.f;
+      for (int i = lane; i < n_f; i += kWave) a2 += __expf(key_s(ws.buf[i]) - m) / z1;
+      const float pp = wave_sum(a2);
+      const float thr = ((__expf(key_s(ws.buf[0]) - m) / z1) / pp) * p.min_p;
+      int cut = n_f;
+      for (int r0 = 0; r0 < n_f; r0 += kWave) {
+        const int i = r0 + lane;
+        const uint64_t hit = __ballot(i < n_f && (__expf(key_s(ws.buf[i]) - m) / z1) / pp < thr);
+        if (hit) {
+          cut = r0 + __ffsll(static_cast<long long>(hit)) - 1;
+          break;
+        }
+      }
+      n_f = cut;
+    }
+    if (n_f > kCap) ovf |= kWhyCap;
+    float a3 = 0.f;
+    for (int i = lane; i < n_f; i += kWave) a3 += __expf(key_s(ws.buf[i]) - m);
+    zf = wave_sum(a3);
+  }
+  if (ovf) {
+    if (lane == 0) {
+      RowRec rr{};
+      rr.m = raw_max;  // x-domain upper bound of the row maximum
+      rr.z = 0.f;
+      rr.flags = kFlagOverflow;
+      rr.why = ovf;
+      a.rec_t[row] = rr;
+      a.list_t[atomic_add_u32(a.list_cnt, 1u)] = static_cast<int32_t>(row);
+    }
+    return;
+  }
+  int32_t* sidx = a.sidx_t + row * kCap;
+  float* sp = a.sp_t + row * kCap;
+  for (int i = lane; i < n_f; i += kWave) {
+    const uint64_t kk = ws.buf[i];
+    sidx[i] = key_idx(kk);
+    sp[i] = __expf(key_s(kk) - m) / zf;
+  }
+  if (lane == 0) {
+    RowRec rr;
+    rr.m = m;
+    rr.z = zf;
+    rr.n = n_f;
+    rr.flags = 0;
+    rr.why = 0;
+    rr.last = n_f > 0 ? ws.buf[n_f - 1] : ~uint64_t(0);
+    rr.p_cand = 0.f;
+    if (cr.tok >= 0) {
+      const float sc = cr.x / t;
+      const uint64_t kc = cand_key(sc, cr.tok);
+      rr.p_cand = (kc >= rr.last && rr.n != 0) ? __expf(sc - rr.m) / rr.z : 0.f;
+    }
+    a.rec_t[row] = rr;
+  }
+}
+
 template <typename TagT, bool kVec, typename CandT, int kPath>
 __global__ __launch_bounds__(kT) void target_scan_kernel(Args a) {
   __shared__ Shared sh;
@@ -1176,7 +1668,7 @@ __global__ __launch_bounds__(kT) void target_scan_kernel(Args a) {
   process_row<TagT, kVec, kPath>(sh, rp, a.vocab, p, f, a.s_t, slice, a.pub_t + row * kNBuf,
                                  a.pubs_t + row * a.s_t * 2, a.cnt_t + row, a.rec_t + row,
                                  a.sidx_t + row * kCap, a.sp_t + row * kCap, cr.tok, cr.x, a.list_cnt,
-                                 a.list_t, static_cast<int32_t>(row), raw_filter_ok(f, a.pnonpos, b), a.hint);
+                                 a.list_t, static_cast<int32_t>(row), raw_filter_ok(f, a.pnonpos, b), a.hint, a.wave);
 }
 
 // First rejected position of request b (width-1 when every drafted token is
@@ -1260,7 +1752,7 @@ __global__ __launch_bounds__(kT) void draft_scan_kernel(Args a) {
   process_row<TagD, kVec, kPath>(sh, rp, a.vocab, p, f, a.s_d, slice, a.pub_d + b * kNBuf,
                                  a.pubs_d + b * a.s_d * 2, a.cnt_d + b, a.rec_d + b, a.sidx_d + b * kCap,
                                  a.sp_d + b * kCap, -1, NAN, a.list_cnt + 1, a.list_d, static_cast<int32_t>(b), true,
-                                 a.hint);
+                                 a.hint, 0);
 }
 
 // Exact support of the rows the scan kernels could not resolve from their
@@ -1686,8 +2178,14 @@ extern "C" int ls_verify_sample(const ls_verify_sample_args* in, void* counters,
     const bool dv = dvec_ok && (x.draft_stride_b * sizeof(DS)) % 16 == 0 && (x.draft_stride_k * sizeof(DS)) % 16 == 0; \
     cand_prep_kernel<TT, CT><<<g_c, rs::kT, 0, st>>>(a);                                                      \
     LS_LAUNCH_CHECK();                                                                                        \
+    a.wave = (a.hint != kHintExactOnly && tv && x.vocab / TT::kPerVec >= int64_t(kWave) * kWaveDepth) ? 1 : 0; \
+    a.wave_only = (a.wave && x.max_top_k > 0 && x.max_top_k <= kWaveMaxRowK) ? 1 : 0;                          \
     if (ev) LS_EVENT(0);                                                                                      \
-    if (a.hint != kHintExactOnly) {                                                                           \
+    if (a.wave) {                                                                                             \
+      target_wave_kernel<TT, CT><<<dim3(static_cast<unsigned>(rows)), kWave, 0, st>>>(a);                    \
+      LS_LAUNCH_CHECK();                                                                                      \
+    }                                                                                                         \
+    if (a.hint != kHintExactOnly && !a.wave_only) {                                                           \
       if (tv) target_scan_kernel<TT, true, CT, kPathRaw><<<g_t, rs::kT, 0, st>>>(a);                         \
       else target_scan_kernel<TT, false, CT, kPathRaw><<<g_t, rs::kT, 0, st>>>(a);                           \
       LS_LAUNCH_CHECK();                                                                                      \
