@@ -20,7 +20,9 @@ namespace {
 
 constexpr int kPT = 256;
 
-__global__ __launch_bounds__(kPT) void penalty_tables_kernel(
+constexpr int kPTT = 1024;  // threads of the table builder (one workgroup per request)
+
+__global__ __launch_bounds__(kPTT) void penalty_tables_kernel(
     const int32_t* __restrict__ hist, int64_t hist_stride, const int32_t* __restrict__ hist_lens, int hist_cap,
     int64_t vocab, int words, const float* __restrict__ freq, const float* __restrict__ pres,
     uint32_t* __restrict__ bits_out, uint32_t* __restrict__ rank_out, int64_t words_stride,
@@ -30,62 +32,72 @@ __global__ __launch_bounds__(kPT) void penalty_tables_kernel(
   uint32_t* bits = lds;              // [words]
   uint32_t* rank = lds + words;      // [words]
   uint32_t* cnt = lds + 2 * words;   // [hist_cap]
-  __shared__ uint32_t wave_tot[kPT / kWave];
+  __shared__ uint32_t wave_tot[kPTT / kWave];
   const int b = blockIdx.x;
   const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1), wid = tid / kWave;
   const int n = hist_lens ? min(max(hist_lens[b], 0), hist_cap) : hist_cap;
   const int32_t* h = hist + static_cast<int64_t>(b) * hist_stride;
 
-  for (int w = tid; w < words; w += kPT) bits[w] = 0;
-  for (int r = tid; r < hist_cap; r += kPT) cnt[r] = 0;
+  for (int w = tid; w < words; w += kPTT) bits[w] = 0;
+  if (freq)
+    for (int r = tid; r < hist_cap; r += kPTT) cnt[r] = 0;
   __syncthreads();
-  for (int i = tid; i < n; i += kPT) {
+  for (int i = tid; i < n; i += kPTT) {
     const int t = h[i];
     if (t >= 0 && t < vocab) atomicOr(&bits[t >> 5], 1u << (t & 31));
   }
   __syncthreads();
-  // Exclusive prefix popcount over words, in chunks of kPT words.
-  uint32_t carry = 0;
-  for (int w0 = 0; w0 < words; w0 += kPT) {
-    const int w = w0 + tid;
-    const uint32_t c = w < words ? __popc(bits[w]) : 0u;
-    uint32_t inc = c;
+  // Exclusive prefix popcount over words: each thread owns a contiguous run
+  // of words, one block-wide scan of the run totals.
+  const int per = (words + kPTT - 1) / kPTT;
+  const int w0 = tid * per;
+  const int w1 = min(words, w0 + per);
+  uint32_t c = 0;
+  for (int w = w0; w < w1; ++w) c += __popc(bits[w]);
+  uint32_t inc = c;
 #pragma unroll
-    for (int o = 1; o < kWave; o <<= 1) {
-      uint32_t v = __shfl_up(inc, o, kWave);
-      if ((tid & (kWave - 1)) >= o) inc += v;
-    }
-    if ((tid & (kWave - 1)) == kWave - 1) wave_tot[tid / kWave] = inc;
-    __syncthreads();
-    uint32_t before = carry;
-    for (int k = 0; k < tid / kWave; ++k) before += wave_tot[k];
-    if (w < words) rank[w] = before + inc - c;
-    uint32_t total = 0;
-    for (int k = 0; k < kPT / kWave; ++k) total += wave_tot[k];
-    carry += total;
-    __syncthreads();
+  for (int o = 1; o < kWave; o <<= 1) {
+    const uint32_t v = __shfl_up(inc, o, kWave);
+    if (lane >= o) inc += v;
   }
-  const uint32_t distinct = carry;
-  for (int i = tid; i < n; i += kPT) {
-    const int t = h[i];
-    if (t >= 0 && t < vocab) {
-      const uint32_t bit = 1u << (t & 31);
-      atomicAdd(&cnt[rank[t >> 5] + __popc(bits[t >> 5] & (bit - 1u))], 1u);
-    }
+  if (lane == kWave - 1) wave_tot[wid] = inc;
+  __syncthreads();
+  uint32_t before = 0, distinct = 0;
+  for (int k = 0; k < kPTT / kWave; ++k) {
+    if (k < wid) before += wave_tot[k];
+    distinct += wave_tot[k];
+  }
+  uint32_t run = before + inc - c;
+  for (int w = w0; w < w1; ++w) {
+    rank[w] = run;
+    run += __popc(bits[w]);
   }
   __syncthreads();
+  // Occurrences per present token (only needed for the frequency penalty).
+  if (freq) {
+    for (int i = tid; i < n; i += kPTT) {
+      const int t = h[i];
+      if (t >= 0 && t < vocab) {
+        const uint32_t bit = 1u << (t & 31);
+        atomicAdd(&cnt[rank[t >> 5] + __popc(bits[t >> 5] & (bit - 1u))], 1u);
+      }
+    }
+    __syncthreads();
+  }
   uint32_t* bo = bits_out + static_cast<int64_t>(b) * words_stride;
   uint32_t* ro = rank_out + static_cast<int64_t>(b) * words_stride;
-  for (int w = tid; w < words; w += kPT) {
+  for (int w = tid; w < words; w += kPTT) {
     bo[w] = bits[w];
     ro[w] = rank[w];
   }
   const float f = freq ? freq[b] : 0.f;
   const float p = pres ? pres[b] : 0.f;
   float* ao = add_out + static_cast<int64_t>(b) * add_stride;
-  for (uint32_t r = tid; r < distinct; r += kPT) {
+  for (uint32_t r = tid; r < distinct; r += kPTT) {
     float acc = 0.f;  // scatter_add_ of `f`, once per occurrence
-    for (uint32_t i = 0; i < cnt[r]; ++i) acc += f;
+    if (freq)
+      for (uint32_t i = 0; i < cnt[r]; ++i) acc += f;
     float a = 0.f - acc;  // additive tensor starts at zero, then sub_ frequency
     a = a - p;            // then sub_ presence
     ao[r] = a;
@@ -142,7 +154,7 @@ extern "C" int ls_penalty_tables(const int32_t* history, int64_t history_stride,
   LS_CHECK(lds <= 64 * 1024, LS_ERR_SHAPE,
            "ls_penalty_tables: vocab %lld with history %d exceeds the 64 KiB LDS budget",
            (long long)vocab, history_cap);
-  penalty_tables_kernel<<<dim3(static_cast<unsigned>(batch)), kPT, lds, static_cast<hipStream_t>(stream)>>>(
+  penalty_tables_kernel<<<dim3(static_cast<unsigned>(batch)), kPTT, lds, static_cast<hipStream_t>(stream)>>>(
       history, history_stride, history_lens, history_cap, vocab, static_cast<int>(words), frequency, presence,
       bits, rank, words_stride, add, add_stride, distinct, nonpositive);
   LS_LAUNCH_CHECK();

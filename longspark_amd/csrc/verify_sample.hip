@@ -98,6 +98,8 @@ struct Args {
   int hint;            // which scan kernels the launcher runs (Hint)
   int wave;            // 1: target_wave_kernel runs (takes raw rows with k <= kWaveMaxK)
   int wave_only;       // 1: no workgroup raw scan follows (the wave kernel lists every other raw row)
+  int dwave;           // 1: draft_wave_kernel runs (takes draft rows that are top-k with k <= kWaveMaxK)
+  int dwave_only;      // 1: no workgroup draft scan follows
   uint32_t* list_cnt;  // counters [2]: rows waiting for the exact fallback (target, draft)
   int32_t* list_t;     // [B*K]
   int32_t* list_d;     // [B]
@@ -1358,62 +1360,34 @@ __device__ __forceinline__ float wave_compact_topk(WaveShared& ws, const XForm& 
   return thr;
 }
 
-template <typename TagT, typename CandT>
-__global__ __launch_bounds__(kWave) void target_wave_kernel(Args a) {
-  __shared__ WaveShared ws;
+// Streams the elements [e_off, e_off + nelem) of a row (rp points at element
+// e_off, 16-byte aligned; e_off a multiple of P) and leaves in ws.buf[0..count)
+// every element that can be among the row range's k largest transformed
+// values: x-domain keys, transformed, compacted to the k largest within the
+// rounding margin.  r and q hold the loads of the first two chunks, issued by
+// the caller.  raw_max is the range's raw maximum (wave-reduced); ovf gets the
+// Why bits of a range that the buffer could not resolve.
+template <typename TagT>
+__device__ __forceinline__ void wave_scan_candidates(WaveShared& ws, const typename TagT::storage* rp, int64_t nelem,
+                                                     int64_t e_off, const XForm& f, int k, uint4 (&r)[kWaveDepth],
+                                                     uint4 (&q)[kWaveDepth], int& count, float& raw_max, int& ovf) {
   using S = typename TagT::storage;
   constexpr int P = TagT::kPerVec;
-  const int64_t row = blockIdx.x;
-  const int64_t b = row / a.width;
-  const int lane = threadIdx.x;
-  const S* rp = static_cast<const S*>(a.logits) + row * a.lrs;
+  constexpr bool kBf16 = __is_same(TagT, BF16);
+  const int lane = threadIdx.x & (kWave - 1);
   const uint4* vp = reinterpret_cast<const uint4*>(rp);
-  const int64_t nfull = a.vocab / P;               // whole 16-byte vectors
+  const int64_t nfull = nelem / P;
   const int64_t steps = (nfull + kWave - 1) / kWave;
   const int64_t last = nfull - 1;
-  // The first chunk is requested before the row's parameters are read, so
-  // its latency overlaps the set-up (a row of another path discards it).
-  uint4 r[kWaveDepth], q[kWaveDepth];
-#pragma unroll
-  for (int u = 0; u < kWaveDepth; ++u) r[u] = load16_stream(vp + min<int64_t>(u * kWave + lane, last));
-#pragma unroll
-  for (int u = 0; u < kWaveDepth; ++u) q[u] = load16_stream(vp + min<int64_t>((kWaveDepth + u) * kWave + lane, last));
-  Params p{a.temps[b], a.top_ks ? max(a.top_ks[b], 1) : static_cast<int>(a.vocab), a.top_ps ? a.top_ps[b] : 1.f,
-           a.min_ps ? a.min_ps[b] : 0.f};
-  const XForm f = target_xform(a, b, row);
-  const int mode = row_mode(p, a.vocab);
-  const bool raw = mode == kModeTopK && raw_filter_ok(f, a.pnonpos, b);
-  if (!(raw && p.top_k <= kWaveMaxK)) {
-    // Rows of the other paths.  In a raw-only launch the rows that are not raw
-    // go to the exact fallback unscanned; raw rows with larger k go there too
-    // when no workgroup raw scan follows.
-    if (((!raw && a.hint == kHintRawOnly) || (raw && a.wave_only)) && lane == 0) {
-      RowRec rr{};
-      rr.flags = kFlagOverflow | kFlagUnscanned;
-      rr.why = kWhyHint;
-      a.rec_t[row] = rr;
-      a.list_t[atomic_add_u32(a.list_cnt, 1u)] = static_cast<int32_t>(row);
-    }
-    return;
-  }
-  const int k = p.top_k;
-  constexpr bool kBf16 = sizeof(S) == 2 && TagT::kPerVec == 8 && !__is_same(TagT, F16);
-  const CandRec cr = a.cand_rec[row];
-  // Chunks of kWaveDepth steps: every chunk's loads are issued together and
-  // consumed in order, so no load stays in flight across the loop's back edge
-  // (a loop-carried register with a pending load makes the compiler drain all
-  // loads, or copy the register, at every iteration).
 
   float tau = -FLT_MAX;
   if (steps >= kWaveDepth) {
-    // Prologue threshold: the k-th largest of the 64 lane maxima over the
-    // first kWaveDepth vectors of each lane, counting only elements the
-    // transform leaves unchanged (bit clear in the penalty bitmap, set in the
-    // mask), is a transformed value of k distinct elements: a lower bound of
-    // the row's k-th largest.
-    // Each lane keeps its 4 largest unchanged elements; the k-th largest of
-    // those 256 values (ties counted) bounds the row's k-th largest from below.
-    // The penalty and mask words are fetched 16 vectors at a time.
+    // Prologue threshold.  Each lane keeps its 4 largest elements of the first
+    // chunk among those the transform leaves unchanged (bit clear in the
+    // penalty bitmap, set in the mask); the k-th largest of those 256 values
+    // (ties counted) is a transformed value of k distinct elements, so it
+    // bounds the range's k-th largest from below.  The penalty and mask words
+    // are fetched 16 vectors at a time.
     float t0 = -INFINITY, t1 = -INFINITY, t2 = -INFINITY, t3 = -INFINITY;
     constexpr int kHalf = 16;
 #pragma unroll
@@ -1427,18 +1401,18 @@ __global__ __launch_bounds__(kWave) void target_wave_kernel(Args a) {
       if (f.pbits) {
 #pragma unroll
         for (int u = 0; u < kHalf; ++u)
-          pw[u] = f.pbits[(static_cast<int64_t>((h * kHalf + u) * kWave + lane) * P) >> 5];
+          pw[u] = f.pbits[(e_off + static_cast<int64_t>((h * kHalf + u) * kWave + lane) * P) >> 5];
       }
       if (f.mbits) {
 #pragma unroll
         for (int u = 0; u < kHalf; ++u)
-          mw[u] = f.mbits[(static_cast<int64_t>((h * kHalf + u) * kWave + lane) * P) >> 5];
+          mw[u] = f.mbits[(e_off + static_cast<int64_t>((h * kHalf + u) * kWave + lane) * P) >> 5];
       }
 #pragma unroll
       for (int u = 0; u < kHalf; ++u) {
         float x[P];
         unpack16<TagT>(r[h * kHalf + u], x);
-        const int sh = static_cast<int>((static_cast<int64_t>((h * kHalf + u) * kWave + lane) * P) & 31);
+        const int sh = static_cast<int>((e_off + static_cast<int64_t>((h * kHalf + u) * kWave + lane) * P) & 31);
         const uint32_t ok = (~pw[u] & mw[u]) >> sh;
 #pragma unroll
         for (int qq = 0; qq < P; ++qq) {
@@ -1461,32 +1435,31 @@ __global__ __launch_bounds__(kWave) void target_wave_kernel(Args a) {
     if (tk > -INFINITY) tau = x_lower(tk);
   }
 
-  int count = 0, ntrans = 0, ovf = 0;
-  float raw_max = -INFINITY;
-  // One step consumes ring slot u (vector st*64 + lane) and refills it with
-  // the vector kWaveDepth steps ahead.  Slots are fixed registers and refills
-  // are unconditional (clamped to the last vector past the end), so no copy
-  // or branch makes the compiler wait for younger loads than the slot's own.
+  count = 0;
+  ovf = 0;
+  raw_max = -INFINITY;
+  int ntrans = 0;
   auto step = [&](float* x, int64_t st) __attribute__((always_inline)) {
     const int64_t idx = st * kWave + lane;
     if (idx >= nfull) {
 #pragma unroll
-      for (int q = 0; q < P; ++q) x[q] = -INFINITY;
+      for (int qq = 0; qq < P; ++qq) x[qq] = -INFINITY;
     }
     float vmax = x[0];
 #pragma unroll
-    for (int q = 1; q < P; ++q) vmax = fmaxf(vmax, x[q]);
+    for (int qq = 1; qq < P; ++qq) vmax = fmaxf(vmax, x[qq]);
     raw_max = fmaxf(raw_max, vmax);
     // Appends past the buffer are dropped and counted; the chunk boundary
     // turns that into an overflow (the row is resolved by the exact fallback).
-    if (__ballot(vmax >= tau)) wave_append<P>(ws, count, x, tau, idx * P);
+    if (__ballot(vmax >= tau)) wave_append<P>(ws, count, x, tau, e_off + idx * P);
   };
-  // Two chunk buffers: while one chunk is consumed the next one is in flight.
-  // Refills are unconditional (clamped to the last vector past the end) so
-  // the buffers need no merge copies; the loop is unrolled by two so each
-  // buffer keeps its registers.  Between chunks, compact once the buffer
-  // holds more than 2k entries, so the threshold follows the running k-th
-  // largest and few elements arrive.
+  // Chunks of kWaveDepth steps in two buffers: while one chunk is consumed the
+  // next one is in flight.  No load stays in flight across the loop's back
+  // edge (a loop-carried register with a pending load makes the compiler
+  // drain every load, or copy the register, at each iteration); refills are
+  // unconditional (clamped to the last vector past the end) so the buffers
+  // need no merge copies.  Between chunks, compact once the buffer holds more
+  // than 2k entries, so the threshold follows the running k-th largest.
   const int soft = max(2 * k, 64);
 #define LS_WAVE_BOUNDARY()                                                 \
   do {                                                                      \
@@ -1495,7 +1468,7 @@ __global__ __launch_bounds__(kWave) void target_wave_kernel(Args a) {
       tau = INFINITY;                                                       \
     } else if (count > soft && !ovf) {                                      \
       wave_sync();                                                          \
-      tau = fmaxf(tau, wave_compact_topk(ws, f, count, ntrans, k, kBf16));         \
+      tau = fmaxf(tau, wave_compact_topk(ws, f, count, ntrans, k, kBf16));  \
       if (count > kWaveTrigger) { ovf = kWhyTies; tau = INFINITY; }         \
     }                                                                       \
   } while (0)
@@ -1527,31 +1500,39 @@ __global__ __launch_bounds__(kWave) void target_wave_kernel(Args a) {
 #undef LS_WAVE_ISSUE
 #undef LS_WAVE_CONSUME
 #undef LS_WAVE_BOUNDARY
-  // Elements past the last whole vector (vocab not a multiple of P).
+  // Elements past the last whole vector (range length not a multiple of P).
   {
     const int64_t v = nfull * P + lane;
-    float x[1] = {v < a.vocab ? to_f32<S>(rp[v]) : -INFINITY};
+    float x[1] = {v < nelem ? to_f32<S>(rp[v]) : -INFINITY};
     raw_max = fmaxf(raw_max, x[0]);
-    if (__ballot(x[0] >= tau)) wave_append<1>(ws, count, x, tau, v);
+    if (__ballot(x[0] >= tau)) wave_append<1>(ws, count, x, tau, e_off + v);
   }
   raw_max = wave_max(raw_max);
   if (count > kWaveBuf) ovf |= kWhyLost;
   wave_sync();
+  if (!ovf) wave_compact_topk(ws, f, count, ntrans, k, kBf16);
+}
 
-  // Final support: keep the k largest transformed values, re-key by x / T.
+// Support of a top-k row from its candidates ws.buf[0..count) (x-domain,
+// transformed, at least the k largest within the margin): re-key by x / T,
+// sort, cut by top-k (ties to the lowest index), top-p and min-p, and write
+// the row record and support.  A row the candidates cannot resolve (ovf) is
+// listed for the exact fallback with its raw maximum.
+__device__ void wave_finalize_topk(WaveShared& ws, int count, const Params& p, float raw_max, int ovf, RowRec* rec,
+                                   int32_t* sidx, float* sp, int cand_tok, float cand_x, uint32_t* list_cnt,
+                                   int32_t* list, int32_t list_id) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int k = p.top_k;
   const float t = p.temperature;
-  if (!ovf) {
-    wave_compact_topk(ws, f, count, ntrans, k, kBf16);
-    for (int i = lane; i < count; i += kWave) {
-      const uint64_t key = ws.buf[i];
-      ws.buf[i] = cand_key(key_s(key) / t, key_idx(key));
-    }
-    wave_sync();
-  }
   int n = count;
   float m = 0.f, zf = 0.f;
   int n_f = 0;
   if (!ovf) {
+    for (int i = lane; i < n; i += kWave) {
+      const uint64_t key = ws.buf[i];
+      ws.buf[i] = cand_key(key_s(key) / t, key_idx(key));
+    }
+    wave_sync();
     if (n <= kWave) {
       // one key per lane: bitonic sort across the wave, descending
       uint64_t key = lane < n ? ws.buf[lane] : 0;
@@ -1620,13 +1601,11 @@ __global__ __launch_bounds__(kWave) void target_wave_kernel(Args a) {
       rr.z = 0.f;
       rr.flags = kFlagOverflow;
       rr.why = ovf;
-      a.rec_t[row] = rr;
-      a.list_t[atomic_add_u32(a.list_cnt, 1u)] = static_cast<int32_t>(row);
+      *rec = rr;
+      list[atomic_add_u32(list_cnt, 1u)] = list_id;
     }
     return;
   }
-  int32_t* sidx = a.sidx_t + row * kCap;
-  float* sp = a.sp_t + row * kCap;
   for (int i = lane; i < n_f; i += kWave) {
     const uint64_t kk = ws.buf[i];
     sidx[i] = key_idx(kk);
@@ -1641,13 +1620,57 @@ __global__ __launch_bounds__(kWave) void target_wave_kernel(Args a) {
     rr.why = 0;
     rr.last = n_f > 0 ? ws.buf[n_f - 1] : ~uint64_t(0);
     rr.p_cand = 0.f;
-    if (cr.tok >= 0) {
-      const float sc = cr.x / t;
-      const uint64_t kc = cand_key(sc, cr.tok);
+    if (cand_tok >= 0) {
+      const float sc = cand_x / t;
+      const uint64_t kc = cand_key(sc, cand_tok);
       rr.p_cand = (kc >= rr.last && rr.n != 0) ? __expf(sc - rr.m) / rr.z : 0.f;
     }
-    a.rec_t[row] = rr;
+    *rec = rr;
   }
+}
+
+template <typename TagT, typename CandT>
+__global__ __launch_bounds__(kWave) void target_wave_kernel(Args a) {
+  __shared__ WaveShared ws;
+  using S = typename TagT::storage;
+  constexpr int P = TagT::kPerVec;
+  const int64_t row = blockIdx.x;
+  const int64_t b = row / a.width;
+  const int lane = threadIdx.x;
+  const S* rp = static_cast<const S*>(a.logits) + row * a.lrs;
+  const uint4* vp = reinterpret_cast<const uint4*>(rp);
+  const int64_t last = a.vocab / P - 1;
+  // The first two chunks are requested before the row's parameters are read,
+  // so their latency overlaps the set-up (a row of another path discards them).
+  uint4 r[kWaveDepth], q[kWaveDepth];
+#pragma unroll
+  for (int u = 0; u < kWaveDepth; ++u) r[u] = load16_stream(vp + min<int64_t>(u * kWave + lane, last));
+#pragma unroll
+  for (int u = 0; u < kWaveDepth; ++u) q[u] = load16_stream(vp + min<int64_t>((kWaveDepth + u) * kWave + lane, last));
+  Params p{a.temps[b], a.top_ks ? max(a.top_ks[b], 1) : static_cast<int>(a.vocab), a.top_ps ? a.top_ps[b] : 1.f,
+           a.min_ps ? a.min_ps[b] : 0.f};
+  const XForm f = target_xform(a, b, row);
+  const int mode = row_mode(p, a.vocab);
+  const bool raw = mode == kModeTopK && raw_filter_ok(f, a.pnonpos, b);
+  if (!(raw && p.top_k <= kWaveMaxK)) {
+    // Rows of the other paths.  In a raw-only launch the rows that are not raw
+    // go to the exact fallback unscanned; raw rows with larger k go there too
+    // when no workgroup raw scan follows.
+    if (((!raw && a.hint == kHintRawOnly) || (raw && a.wave_only)) && lane == 0) {
+      RowRec rr{};
+      rr.flags = kFlagOverflow | kFlagUnscanned;
+      rr.why = kWhyHint;
+      a.rec_t[row] = rr;
+      a.list_t[atomic_add_u32(a.list_cnt, 1u)] = static_cast<int32_t>(row);
+    }
+    return;
+  }
+  const CandRec cr = a.cand_rec[row];
+  int count, ovf;
+  float raw_max;
+  wave_scan_candidates<TagT>(ws, rp, a.vocab, 0, f, p.top_k, r, q, count, raw_max, ovf);
+  wave_finalize_topk(ws, count, p, raw_max, ovf, a.rec_t + row, a.sidx_t + row * kCap, a.sp_t + row * kCap, cr.tok,
+                     cr.x, a.list_cnt, a.list_t, static_cast<int32_t>(row));
 }
 
 template <typename TagT, bool kVec, typename CandT, int kPath>
@@ -1675,7 +1698,7 @@ __global__ __launch_bounds__(kT) void target_scan_kernel(Args a) {
 // accepted) and blocking flags, from the target row records.  Called by all
 // 64 lanes of one wave (lane j tests position j); every lane gets the result.
 template <typename CandT>
-__device__ int accept_length_wave(const Args& a, int64_t b, int* flags) {
+__device__ __forceinline__ int accept_length_wave(const Args& a, int64_t b, int* flags) {
   const int g = a.width - 1;
   const int lane = threadIdx.x & (kWave - 1);
   for (int base = 0; base < g; base += kWave) {
@@ -1747,12 +1770,117 @@ __global__ __launch_bounds__(kT) void draft_scan_kernel(Args a) {
   p.top_p = a.d_top_ps ? a.d_top_ps[b] : 1.f;
   p.min_p = a.d_min_ps ? a.d_min_ps[b] : 0.f;
   using S = typename TagD::storage;
+  if (a.dwave && row_mode(p, a.vocab) == kModeTopK && p.top_k <= kWaveMaxK) return;  // draft_wave_kernel's row
   const S* rp = static_cast<const S*>(a.draft) + b * a.dsb + static_cast<int64_t>(len) * a.dsk;
   XForm f{nullptr, nullptr, nullptr, 1.f, 0, nullptr};
   process_row<TagD, kVec, kPath>(sh, rp, a.vocab, p, f, a.s_d, slice, a.pub_d + b * kNBuf,
                                  a.pubs_d + b * a.s_d * 2, a.cnt_d + b, a.rec_d + b, a.sidx_d + b * kCap,
                                  a.sp_d + b * kCap, -1, NAN, a.list_cnt + 1, a.list_d, static_cast<int32_t>(b), true,
                                  a.hint, 0);
+}
+
+// Draft rows: kDraftSlices wavefronts per rejected request each scan one
+// slice of the fp32 draft row at the rejection position, keep the slice's k
+// largest (within the margin) and publish them; the last slice to arrive
+// gathers every slice's candidates, keeps the row's k largest and finalises
+// the row.  Hand-off through agent-scope atomics on caller workspace (the
+// counter returns to zero), as in the workgroup slice merge.
+constexpr int kDraftSlices = 16;
+constexpr int kDraftCap = kWaveBuf / kDraftSlices;  // published candidates per slice
+
+template <typename TagD, typename CandT>
+__global__ __launch_bounds__(kWave) void draft_wave_kernel(Args a) {
+  __shared__ WaveShared ws;
+  using S = typename TagD::storage;
+  constexpr int P = TagD::kPerVec;
+  const int64_t b = blockIdx.x / kDraftSlices;
+  const int slice = blockIdx.x % kDraftSlices;
+  const int lane = threadIdx.x;
+  int fl;
+  const int len = accept_length_wave<CandT>(a, b, &fl);
+  if (len >= a.width - 1 || fl) {
+    if (slice == 0 && lane == 0) {
+      RowRec rr{};
+      rr.flags = kFlagSkip;
+      a.rec_d[b] = rr;
+    }
+    return;
+  }
+  Params p;
+  p.temperature = a.d_temps ? a.d_temps[b] : a.temps[b];
+  p.top_k = a.d_top_ks ? max(a.d_top_ks[b], 1) : static_cast<int>(a.vocab);
+  p.top_p = a.d_top_ps ? a.d_top_ps[b] : 1.f;
+  p.min_p = a.d_min_ps ? a.d_min_ps[b] : 0.f;
+  const bool topk = row_mode(p, a.vocab) == kModeTopK;
+  if (!(topk && p.top_k <= kWaveMaxK)) {
+    // A draft row of another path: the workgroup draft scan takes it, or,
+    // when none follows, the exact draft fallback does.
+    if (a.dwave_only && slice == 0 && lane == 0) {
+      RowRec rr{};
+      rr.flags = kFlagOverflow | kFlagUnscanned;
+      rr.why = kWhyHint;
+      a.rec_d[b] = rr;
+      a.list_d[atomic_add_u32(a.list_cnt + 1, 1u)] = static_cast<int32_t>(b);
+    }
+    return;
+  }
+  const S* row = static_cast<const S*>(a.draft) + b * a.dsb + static_cast<int64_t>(len) * a.dsk;
+  const SliceRange sr = slice_range(a.vocab, kDraftSlices, slice, P);
+  const S* rp = row + sr.v_begin;
+  const int64_t nelem = sr.v_end - sr.v_begin;
+  const uint4* vp = reinterpret_cast<const uint4*>(rp);
+  const int64_t last = max<int64_t>(nelem / P - 1, 0);
+  uint4 r[kWaveDepth], q[kWaveDepth];
+#pragma unroll
+  for (int u = 0; u < kWaveDepth; ++u) r[u] = load16_stream(vp + min<int64_t>(u * kWave + lane, last));
+#pragma unroll
+  for (int u = 0; u < kWaveDepth; ++u) q[u] = load16_stream(vp + min<int64_t>((kWaveDepth + u) * kWave + lane, last));
+  const XForm f{nullptr, nullptr, nullptr, 1.f, 0, nullptr};
+  int count, ovf;
+  float raw_max;
+  wave_scan_candidates<TagD>(ws, rp, nelem, sr.v_begin, f, p.top_k, r, q, count, raw_max, ovf);
+
+  // Publish this slice, arrive; the last slice gathers the row.
+  uint64_t* pub = a.pub_d + b * kNBuf + static_cast<int64_t>(slice) * kDraftCap;
+  uint64_t* pubs = a.pubs_d + b * 2 * kDraftSlices;
+  const bool bad = ovf || count > kDraftCap;
+  if (!bad)
+    for (int i = lane; i < count; i += kWave) atomic_put_u64(pub + i, ws.buf[i]);
+  int last_slice = 0;
+  if (lane == 0) {
+    atomic_put_u64(pubs + 2 * slice, bad ? ~uint64_t(0) : static_cast<uint64_t>(count));
+    atomic_put_u64(pubs + 2 * slice + 1, static_cast<uint64_t>(ordered_f32(raw_max)));
+    last_slice = arrive(a.cnt_d + b) == static_cast<uint32_t>(kDraftSlices - 1);
+  }
+  last_slice = __shfl(last_slice, 0, kWave);
+  if (!last_slice) return;
+  if (lane == 0) atomic_take_u32(a.cnt_d + b);
+  // lane s < kDraftSlices takes slice s's count and maximum
+  uint64_t c = 0;
+  float smx = -FLT_MAX;
+  if (lane < kDraftSlices) {
+    c = atomic_take_u64(pubs + 2 * lane);
+    smx = unordered_f32(static_cast<uint32_t>(atomic_take_u64(pubs + 2 * lane + 1)));
+  }
+  const bool any_bad = __ballot(lane < kDraftSlices && c == ~uint64_t(0)) != 0;
+  const int cnt = (lane < kDraftSlices && c != ~uint64_t(0)) ? static_cast<int>(c) : 0;
+  int total;
+  const int off = wave_excl_scan(cnt, &total);
+  raw_max = wave_max(smx);
+  int merged_ovf = (any_bad || total > kWaveBuf) ? kWhyMerge : 0;
+  if (!merged_ovf) {
+    for (int s2 = 0; s2 < kDraftSlices; ++s2) {
+      const int base = __shfl(off, s2, kWave), n2 = __shfl(cnt, s2, kWave);
+      const uint64_t* src = a.pub_d + b * kNBuf + static_cast<int64_t>(s2) * kDraftCap;
+      for (int i = lane; i < n2; i += kWave) ws.buf[base + i] = atomic_take_u64(const_cast<uint64_t*>(src) + i);
+    }
+    wave_sync();
+    int ntrans = total;
+    count = total;
+    wave_compact_topk(ws, f, count, ntrans, p.top_k, false);
+  }
+  wave_finalize_topk(ws, count, p, raw_max, merged_ovf, a.rec_d + b, a.sidx_d + b * kCap, a.sp_d + b * kCap, -1,
+                     NAN, a.list_cnt + 1, a.list_d, static_cast<int32_t>(b));
 }
 
 // Exact support of the rows the scan kernels could not resolve from their
@@ -2068,8 +2196,8 @@ Layout layout(int64_t batch, int width, int64_t vocab, int max_top_k) {
   l.off_sp_d = o; o += up256(4ull * batch * kCap);
   l.off_pub_t = o; o += l.s_t > 1 ? up256(8ull * rows * kNBuf) : 0;
   l.off_pubs_t = o; o += up256(16ull * rows * l.s_t);
-  l.off_pub_d = o; o += l.s_d > 1 ? up256(8ull * batch * kNBuf) : 0;
-  l.off_pubs_d = o; o += up256(16ull * batch * l.s_d);
+  l.off_pub_d = o; o += up256(8ull * batch * kNBuf);  // workgroup and wavefront slice hand-off
+  l.off_pubs_d = o; o += up256(16ull * batch * (l.s_d > kDraftSlices ? l.s_d : kDraftSlices));
   l.off_list_t = o; o += up256(4ull * rows);
   l.off_list_d = o; o += up256(4ull * batch);
   l.off_cand = o; o += up256(sizeof(CandRec) * rows);
@@ -2156,6 +2284,7 @@ extern "C" int ls_verify_sample(const ls_verify_sample_args* in, void* counters,
   a.s_t = l.s_t;
   a.s_d = l.s_d;
   a.hint = x.scan_hint;
+  a.wave = a.wave_only = a.dwave = a.dwave_only = 0;
   hipStream_t st = static_cast<hipStream_t>(stream);
 
   const dim3 g_t(static_cast<unsigned>(rows * l.s_t)), g_d(static_cast<unsigned>(x.batch * l.s_d)),
@@ -2199,12 +2328,19 @@ extern "C" int ls_verify_sample(const ls_verify_sample_args* in, void* counters,
     target_fallback_kernel<TT, CT><<<g_f, rs::kT, 0, st>>>(a);                                                \
     LS_LAUNCH_CHECK();                                                                                        \
     if (x.q_mode == 0) {                                                                                      \
-      if (a.hint != kHintExactOnly) {                                                                         \
+      a.dwave = (a.hint != kHintExactOnly && dv &&                                                            \
+                 x.vocab / kDraftSlices / TD::kPerVec >= int64_t(kWave) * kWaveDepth) ? 1 : 0;               \
+      a.dwave_only = (a.dwave && x.max_top_k > 0 && x.max_top_k <= kWaveMaxRowK) ? 1 : 0;                     \
+      if (a.dwave) {                                                                                          \
+        draft_wave_kernel<TD, CT><<<dim3(static_cast<unsigned>(x.batch * kDraftSlices)), kWave, 0, st>>>(a);  \
+        LS_LAUNCH_CHECK();                                                                                    \
+      }                                                                                                       \
+      if (a.hint != kHintExactOnly && !a.dwave_only) {                                                        \
         if (dv) draft_scan_kernel<TD, true, CT, kPathRaw><<<g_d, rs::kT, 0, st>>>(a);                        \
         else draft_scan_kernel<TD, false, CT, kPathRaw><<<g_d, rs::kT, 0, st>>>(a);                          \
         LS_LAUNCH_CHECK();                                                                                    \
       }                                                                                                       \
-      if (a.hint != kHintRawOnly) {                                                                           \
+      if (a.hint != kHintRawOnly && !a.dwave_only) {                                                          \
         if (dv) draft_scan_kernel<TD, true, CT, kPathExact><<<g_d, rs::kT, 0, st>>>(a);                      \
         else draft_scan_kernel<TD, false, CT, kPathExact><<<g_d, rs::kT, 0, st>>>(a);                        \
         LS_LAUNCH_CHECK();                                                                                    \
