@@ -126,6 +126,11 @@ __device__ __forceinline__ float wave_sum(float v) {
   for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
   return v;
 }
+__device__ __forceinline__ int wave_max_i(int v) {
+#pragma unroll
+  for (int o = kWave / 2; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o, kWave));
+  return v;
+}
 __device__ __forceinline__ int wave_sum_i(int v) {
 #pragma unroll
   for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
@@ -194,6 +199,12 @@ __device__ __forceinline__ uint64_t atomic_take_u64(uint64_t* p) {
 }
 __device__ __forceinline__ uint32_t atomic_take_u32(uint32_t* p) {
   return __hip_atomic_exchange(p, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Current value of a word published by atomic RMWs: an agent-scope atomic
+// load (a coherent load, served from the coherence point and not from a
+// stale line of the reader's L2), which leaves the word unchanged.
+__device__ __forceinline__ uint64_t atomic_peek_u64(const uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 // Arrive on a counter after this thread's prior atomics completed; returns
 // the previous count.

@@ -100,6 +100,9 @@ struct Args {
   int wave_only;       // 1: no workgroup raw scan follows (the wave kernel lists every other raw row)
   int dwave;           // 1: draft_wave_kernel runs (takes draft rows that are top-k with k <= kWaveMaxK)
   int dwave_only;      // 1: no workgroup draft scan follows
+  int fuse_draft;      // 1: verify_wave_kernel's grid also carries the draft slices (after the target rows)
+  int dslices;         // wavefront draft slices per request (<= kDraftSlices)
+  uint64_t* acc_t;     // [B*K] acceptance word of each target row (fused launch; zero when not published)
   uint32_t* list_cnt;  // counters [2]: rows waiting for the exact fallback (target, draft)
   int32_t* list_t;     // [B*K]
   int32_t* list_d;     // [B]
@@ -138,6 +141,7 @@ enum Why : int {
   kWhyCap = 64,       // support larger than a record holds
   kWhyHint = 128,     // raw-only launch: row needs the exact path, never scanned
   kWhyExact = 256,    // record written by the fallback
+  kWhyDefer = 512,    // draft row: acceptance not known when its slices ran (resolve takes it)
 };
 
 // A lower bound of the k-th largest (ties counted) of the kT values v (one
@@ -1249,15 +1253,46 @@ __device__ __forceinline__ void wave_transform(WaveShared& ws, const XForm& f, i
   wave_sync();
 }
 
-// Ordered-s of the k-th largest of buf[0..n) (ties counted), 1 <= k <= n,
-// by an MSB-first radix select over 8-bit digits.  With bf16_keys every key
-// holds a bf16 value, whose ordered form has its low 16 bits all 0 (positive)
-// or all 1 (negative): two passes then fix the whole value.
-__device__ uint32_t wave_select_kth(WaveShared& ws, int n, int k, bool bf16_keys = false) {
+// k-th largest (ties counted) of the R*64 ordered values o held R per lane,
+// 1 <= k <= R*64, decided bit by bit from the top: the largest t with at
+// least k values >= t.  Bits below low_bit are left 0 (the result is then the
+// k-th largest's high bits, a value no larger).  Counting uses ballots only.
+template <int R>
+__device__ __forceinline__ uint32_t wave_kth_ballot(const uint32_t (&o)[R], int k, int low_bit) {
+  uint32_t t = 0;
+  for (int bit = 31; bit >= low_bit; --bit) {
+    const uint32_t cand = t | (1u << bit);
+    int c = 0;
+#pragma unroll
+    for (int j = 0; j < R; ++j) c += __popcll(__ballot(o[j] >= cand));
+    if (c >= k) t = cand;
+  }
+  return t;
+}
+
+// Ordered-s of the k-th largest of buf[0..n) (ties counted), 1 <= k <= n:
+// up to 256 entries by ballot counting in registers, more by an MSB-first
+// radix select over 8-bit digits.  With bf16_keys every key holds a bf16
+// value, whose ordered form has its low 16 bits all 0 (positive) or all 1
+// (negative): the top 16 bits then fix the whole value.  With prefix16 (fp32
+// keys) only the k-th largest's top 16 bits are found, returned with the low
+// 16 bits cleared: an ordered value no larger than the k-th largest.
+__device__ uint32_t wave_select_kth(WaveShared& ws, int n, int k, bool bf16_keys = false, bool prefix16 = false) {
   const int lane = threadIdx.x & (kWave - 1);
+  if (n <= 4 * kWave) {
+    uint32_t o[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int i = j * kWave + lane;
+      o[j] = i < n ? static_cast<uint32_t>(ws.buf[i] >> 32) : 0u;  // 0: below every value (a NaN's form)
+    }
+    uint32_t t = wave_kth_ballot<4>(o, k, (bf16_keys || prefix16) ? 16 : 0);
+    if (bf16_keys) t |= (t & 0x80000000u) ? 0u : 0xFFFFu;
+    return t;
+  }
   uint32_t prefix = 0, pmask = 0;
   int remaining = k;
-  const int passes = bf16_keys ? 2 : 4;
+  const int passes = (bf16_keys || prefix16) ? 2 : 4;
   for (int pass = 0; pass < passes; ++pass) {
     const int shift = 24 - 8 * pass;
 #pragma unroll
@@ -1346,14 +1381,16 @@ __device__ void wave_sort_desc(WaveShared& ws, int n) {
 }
 
 // Transform what is pending, then keep the k largest (within the rounding
-// margin); returns the new raw threshold (or -FLT_MAX if n <= k).
+// margin); returns the new raw threshold (or -FLT_MAX if n <= k).  kth (if
+// given) gets the k-th largest value (ties counted) when n > k.
 __device__ __forceinline__ float wave_compact_topk(WaveShared& ws, const XForm& f, int& count, int& ntrans, int k,
-                                                  bool bf16_raw) {
+                                                  bool bf16_raw, float* kth = nullptr) {
   wave_transform(ws, f, ntrans, count);
   ntrans = count;
   if (count <= k) return -FLT_MAX;
   // penalties change values; the mask only sets -inf (a bf16 value)
   const float xk = unordered_f32(wave_select_kth(ws, count, k, bf16_raw && !f.pbits));
+  if (kth) *kth = xk;
   const float thr = x_lower(xk);
   count = wave_compact_ge(ws, count, ordered_f32(thr));
   ntrans = count;
@@ -1365,12 +1402,15 @@ __device__ __forceinline__ float wave_compact_topk(WaveShared& ws, const XForm& 
 // every element that can be among the row range's k largest transformed
 // values: x-domain keys, transformed, compacted to the k largest within the
 // rounding margin.  r and q hold the loads of the first two chunks, issued by
-// the caller.  raw_max is the range's raw maximum (wave-reduced); ovf gets the
-// Why bits of a range that the buffer could not resolve.
+// the caller.  raw_max is the range's raw maximum (wave-reduced); kth the
+// range's k-th largest transformed value when more than k candidates were
+// left (else -inf); ovf gets the Why bits of a range that the buffer could
+// not resolve.
 template <typename TagT>
 __device__ __forceinline__ void wave_scan_candidates(WaveShared& ws, const typename TagT::storage* rp, int64_t nelem,
                                                      int64_t e_off, const XForm& f, int k, uint4 (&r)[kWaveDepth],
-                                                     uint4 (&q)[kWaveDepth], int& count, float& raw_max, int& ovf) {
+                                                     uint4 (&q)[kWaveDepth], int& count, float& raw_max, float& kth,
+                                                     int& ovf) {
   using S = typename TagT::storage;
   constexpr int P = TagT::kPerVec;
   constexpr bool kBf16 = __is_same(TagT, BF16);
@@ -1426,12 +1466,8 @@ __device__ __forceinline__ void wave_scan_candidates(WaveShared& ws, const typen
         }
       }
     }
-    ws.buf[4 * lane + 0] = cand_key(t0, 0);
-    ws.buf[4 * lane + 1] = cand_key(t1, 0);
-    ws.buf[4 * lane + 2] = cand_key(t2, 0);
-    ws.buf[4 * lane + 3] = cand_key(t3, 0);
-    wave_sync();
-    const float tk = unordered_f32(wave_select_kth(ws, 4 * kWave, k));
+    const uint32_t o[4] = {ordered_f32(t0), ordered_f32(t1), ordered_f32(t2), ordered_f32(t3)};
+    const float tk = unordered_f32(wave_kth_ballot<4>(o, k, 0));
     if (tk > -INFINITY) tau = x_lower(tk);
   }
 
@@ -1510,15 +1546,17 @@ __device__ __forceinline__ void wave_scan_candidates(WaveShared& ws, const typen
   raw_max = wave_max(raw_max);
   if (count > kWaveBuf) ovf |= kWhyLost;
   wave_sync();
-  if (!ovf) wave_compact_topk(ws, f, count, ntrans, k, kBf16);
+  kth = -INFINITY;
+  if (!ovf) wave_compact_topk(ws, f, count, ntrans, k, kBf16, &kth);
 }
 
 // Support of a top-k row from its candidates ws.buf[0..count) (x-domain,
 // transformed, at least the k largest within the margin): re-key by x / T,
 // sort, cut by top-k (ties to the lowest index), top-p and min-p, and write
 // the row record and support.  A row the candidates cannot resolve (ovf) is
-// listed for the exact fallback with its raw maximum.
-__device__ void wave_finalize_topk(WaveShared& ws, int count, const Params& p, float raw_max, int ovf, RowRec* rec,
+// listed for the exact fallback with its raw maximum.  Returns, in lane 0,
+// the row's acceptance word: flags << 32 | bits(p_cand).
+__device__ uint64_t wave_finalize_topk(WaveShared& ws, int count, const Params& p, float raw_max, int ovf, RowRec* rec,
                                    int32_t* sidx, float* sp, int cand_tok, float cand_x, uint32_t* list_cnt,
                                    int32_t* list, int32_t list_id) {
   const int lane = threadIdx.x & (kWave - 1);
@@ -1604,7 +1642,7 @@ __device__ void wave_finalize_topk(WaveShared& ws, int count, const Params& p, f
       *rec = rr;
       list[atomic_add_u32(list_cnt, 1u)] = list_id;
     }
-    return;
+    return static_cast<uint64_t>(kFlagOverflow) << 32;
   }
   for (int i = lane; i < n_f; i += kWave) {
     const uint64_t kk = ws.buf[i];
@@ -1626,51 +1664,9 @@ __device__ void wave_finalize_topk(WaveShared& ws, int count, const Params& p, f
       rr.p_cand = (kc >= rr.last && rr.n != 0) ? __expf(sc - rr.m) / rr.z : 0.f;
     }
     *rec = rr;
+    return __float_as_uint(rr.p_cand);
   }
-}
-
-template <typename TagT, typename CandT>
-__global__ __launch_bounds__(kWave) void target_wave_kernel(Args a) {
-  __shared__ WaveShared ws;
-  using S = typename TagT::storage;
-  constexpr int P = TagT::kPerVec;
-  const int64_t row = blockIdx.x;
-  const int64_t b = row / a.width;
-  const int lane = threadIdx.x;
-  const S* rp = static_cast<const S*>(a.logits) + row * a.lrs;
-  const uint4* vp = reinterpret_cast<const uint4*>(rp);
-  const int64_t last = a.vocab / P - 1;
-  // The first two chunks are requested before the row's parameters are read,
-  // so their latency overlaps the set-up (a row of another path discards them).
-  uint4 r[kWaveDepth], q[kWaveDepth];
-#pragma unroll
-  for (int u = 0; u < kWaveDepth; ++u) r[u] = load16_stream(vp + min<int64_t>(u * kWave + lane, last));
-#pragma unroll
-  for (int u = 0; u < kWaveDepth; ++u) q[u] = load16_stream(vp + min<int64_t>((kWaveDepth + u) * kWave + lane, last));
-  Params p{a.temps[b], a.top_ks ? max(a.top_ks[b], 1) : static_cast<int>(a.vocab), a.top_ps ? a.top_ps[b] : 1.f,
-           a.min_ps ? a.min_ps[b] : 0.f};
-  const XForm f = target_xform(a, b, row);
-  const int mode = row_mode(p, a.vocab);
-  const bool raw = mode == kModeTopK && raw_filter_ok(f, a.pnonpos, b);
-  if (!(raw && p.top_k <= kWaveMaxK)) {
-    // Rows of the other paths.  In a raw-only launch the rows that are not raw
-    // go to the exact fallback unscanned; raw rows with larger k go there too
-    // when no workgroup raw scan follows.
-    if (((!raw && a.hint == kHintRawOnly) || (raw && a.wave_only)) && lane == 0) {
-      RowRec rr{};
-      rr.flags = kFlagOverflow | kFlagUnscanned;
-      rr.why = kWhyHint;
-      a.rec_t[row] = rr;
-      a.list_t[atomic_add_u32(a.list_cnt, 1u)] = static_cast<int32_t>(row);
-    }
-    return;
-  }
-  const CandRec cr = a.cand_rec[row];
-  int count, ovf;
-  float raw_max;
-  wave_scan_candidates<TagT>(ws, rp, a.vocab, 0, f, p.top_k, r, q, count, raw_max, ovf);
-  wave_finalize_topk(ws, count, p, raw_max, ovf, a.rec_t + row, a.sidx_t + row * kCap, a.sp_t + row * kCap, cr.tok,
-                     cr.x, a.list_cnt, a.list_t, static_cast<int32_t>(row));
+  return 0;
 }
 
 template <typename TagT, bool kVec, typename CandT, int kPath>
@@ -1692,6 +1688,17 @@ __global__ __launch_bounds__(kT) void target_scan_kernel(Args a) {
                                  a.pubs_t + row * a.s_t * 2, a.cnt_t + row, a.rec_t + row,
                                  a.sidx_t + row * kCap, a.sp_t + row * kCap, cr.tok, cr.x, a.list_cnt,
                                  a.list_t, static_cast<int32_t>(row), raw_filter_ok(f, a.pnonpos, b), a.hint, a.wave);
+}
+
+// Sampling parameters of request b's draft row (the target's temperature
+// when no draft temperature is given; no filter when a value is absent).
+__device__ __forceinline__ Params draft_params(const Args& a, int64_t b) {
+  Params p;
+  p.temperature = a.d_temps ? a.d_temps[b] : a.temps[b];
+  p.top_k = a.d_top_ks ? max(a.d_top_ks[b], 1) : static_cast<int>(a.vocab);
+  p.top_p = a.d_top_ps ? a.d_top_ps[b] : 1.f;
+  p.min_p = a.d_min_ps ? a.d_min_ps[b] : 0.f;
+  return p;
 }
 
 // First rejected position of request b (width-1 when every drafted token is
@@ -1764,11 +1771,7 @@ __global__ __launch_bounds__(kT) void draft_scan_kernel(Args a) {
     }
     return;
   }
-  Params p;
-  p.temperature = a.d_temps ? a.d_temps[b] : a.temps[b];
-  p.top_k = a.d_top_ks ? max(a.d_top_ks[b], 1) : static_cast<int>(a.vocab);
-  p.top_p = a.d_top_ps ? a.d_top_ps[b] : 1.f;
-  p.min_p = a.d_min_ps ? a.d_min_ps[b] : 0.f;
+  const Params p = draft_params(a, b);
   using S = typename TagD::storage;
   if (a.dwave && row_mode(p, a.vocab) == kModeTopK && p.top_k <= kWaveMaxK) return;  // draft_wave_kernel's row
   const S* rp = static_cast<const S*>(a.draft) + b * a.dsb + static_cast<int64_t>(len) * a.dsk;
@@ -1780,41 +1783,75 @@ __global__ __launch_bounds__(kT) void draft_scan_kernel(Args a) {
 }
 
 // Draft rows: kDraftSlices wavefronts per rejected request each scan one
-// slice of the fp32 draft row at the rejection position, keep the slice's k
-// largest (within the margin) and publish them; the last slice to arrive
-// gathers every slice's candidates, keeps the row's k largest and finalises
-// the row.  Hand-off through agent-scope atomics on caller workspace (the
-// counter returns to zero), as in the workgroup slice merge.
-constexpr int kDraftSlices = 16;
-constexpr int kDraftCap = kWaveBuf / kDraftSlices;  // published candidates per slice
+// slice of the draft row at the rejection position, keep the slice's k
+// largest (within the margin) and publish them to caller workspace; the
+// resolve kernel gathers the slices, keeps the row's k largest and finalises
+// the row.
+constexpr int kDraftSlices = 32;                  // most slices per request (a.dslices: this launch's)
+constexpr int kDraftMinSlices = 16;               // fewest for the wavefront draft path
+constexpr int kDraftCap = kNBuf / kDraftSlices;  // published candidates per slice (a hand-off row each request)
 
-template <typename TagD, typename CandT>
-__global__ __launch_bounds__(kWave) void draft_wave_kernel(Args a) {
-  __shared__ WaveShared ws;
+// Codes a draft slice publishes in place of its candidate count.
+constexpr uint64_t kPubBad = ~uint64_t(0);        // candidates did not fit the hand-off
+constexpr uint64_t kPubDefer = ~uint64_t(0) - 1;  // acceptance not known here: resolve takes the row
+constexpr uint64_t kPubSkip = ~uint64_t(0) - 2;   // every drafted token accepted: no draft row needed
+
+// Acceptance word of a target row in a fused launch: kAccPublished |
+// flags << 32 | bits(p_cand).  The words start at zero (caller-zeroed
+// counter workspace) and the resolve kernel returns them to zero.
+constexpr uint64_t kAccPublished = uint64_t(1) << 63;
+
+// Polls of a fused draft slice waiting for one target row (each poll sleeps
+// about 512 cycles after a load): the wait ends within about a second, and
+// the request's draft row then goes to the exact pass in resolve.
+constexpr int kPollLimit = 1 << 19;
+
+// Accepted length of request b for a draft slice of the fused launch: walks
+// the drafted positions in order, waiting for each target row's acceptance
+// word, and stops at the first rejection (width-1: none), so a request that
+// rejects early waits only for the rows up to the rejection.  -1: not decided
+// here (a row up to the rejection went to the exact fallback, or the wait
+// limit passed).  qv / uv: lane j's draft probability and uniform of
+// position j (width <= 64, so one position per lane).
+__device__ __forceinline__ int fused_accept_length(const Args& a, int64_t b, float qv, float uv) {
+  const int g = a.width - 1;
+  const uint64_t* acc = a.acc_t + b * a.width;
+  int j = 0;
+  for (int it = 0; it < kPollLimit && j < g; ++it) {
+    const uint64_t w0 = atomic_peek_u64(acc + j);  // one address: one load for the wave
+    const uint64_t w = (static_cast<uint64_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(w0 >> 32))) << 32) |
+                       __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(w0));
+    if (!(w & kAccPublished)) {
+      __builtin_amdgcn_s_sleep(8);
+      continue;
+    }
+    if (static_cast<uint32_t>(w >> 32) & kFlagOverflow) return -1;
+    const float q = __shfl(qv, j, kWave), u = __shfl(uv, j, kWave);
+    if (!(u * q < __uint_as_float(static_cast<uint32_t>(w)))) return j;
+    ++j;
+  }
+  return j < g ? -1 : g;
+}
+
+// One draft slice (one wavefront) of request b.  kFused: the slice runs in
+// the target launch and takes the accepted length from the published
+// acceptance words; otherwise from the final target records.
+template <typename TagD, typename CandT, bool kFused>
+__device__ __forceinline__ void draft_wave_slice(const Args& a, WaveShared& ws, int64_t b, int slice) {
   using S = typename TagD::storage;
   constexpr int P = TagD::kPerVec;
-  const int64_t b = blockIdx.x / kDraftSlices;
-  const int slice = blockIdx.x % kDraftSlices;
   const int lane = threadIdx.x;
-  int fl;
-  const int len = accept_length_wave<CandT>(a, b, &fl);
-  if (len >= a.width - 1 || fl) {
-    if (slice == 0 && lane == 0) {
-      RowRec rr{};
-      rr.flags = kFlagSkip;
-      a.rec_d[b] = rr;
-    }
-    return;
+  const int g = a.width - 1;
+  float qv = 0.f, uv = 0.f;
+  if (kFused && lane < g) {
+    qv = a.dtp[b * a.dtp_sb + lane];
+    uv = a.uni[b * a.usb + lane];
   }
-  Params p;
-  p.temperature = a.d_temps ? a.d_temps[b] : a.temps[b];
-  p.top_k = a.d_top_ks ? max(a.d_top_ks[b], 1) : static_cast<int>(a.vocab);
-  p.top_p = a.d_top_ps ? a.d_top_ps[b] : 1.f;
-  p.min_p = a.d_min_ps ? a.d_min_ps[b] : 0.f;
+  const Params p = draft_params(a, b);
   const bool topk = row_mode(p, a.vocab) == kModeTopK;
   if (!(topk && p.top_k <= kWaveMaxK)) {
     // A draft row of another path: the workgroup draft scan takes it, or,
-    // when none follows, the exact draft fallback does.
+    // when none follows, the exact pass in resolve does.
     if (a.dwave_only && slice == 0 && lane == 0) {
       RowRec rr{};
       rr.flags = kFlagOverflow | kFlagUnscanned;
@@ -1824,63 +1861,208 @@ __global__ __launch_bounds__(kWave) void draft_wave_kernel(Args a) {
     }
     return;
   }
-  const S* row = static_cast<const S*>(a.draft) + b * a.dsb + static_cast<int64_t>(len) * a.dsk;
-  const SliceRange sr = slice_range(a.vocab, kDraftSlices, slice, P);
-  const S* rp = row + sr.v_begin;
-  const int64_t nelem = sr.v_end - sr.v_begin;
+  uint64_t code;  // candidate count, or a kPub code
+  int count = 0, ovf = 0;
+  float raw_max = -FLT_MAX, kth = -INFINITY;
+  const XForm f{nullptr, nullptr, nullptr, 1.f, 0, nullptr};
+  int len;
+  if constexpr (kFused) {
+    len = fused_accept_length(a, b, qv, uv);
+  } else {
+    int fl;
+    len = accept_length_wave<CandT>(a, b, &fl);
+    if (len >= g || fl) {
+      // the same outcome in every slice: slice 0 writes it
+      if (slice == 0 && lane == 0) {
+        RowRec rr{};
+        rr.flags = kFlagSkip;
+        a.rec_d[b] = rr;
+      }
+      return;
+    }
+  }
+  if (len < 0) {
+    code = kPubDefer;
+  } else if (len >= g) {
+    code = kPubSkip;
+  } else {
+    const S* row = static_cast<const S*>(a.draft) + b * a.dsb + static_cast<int64_t>(len) * a.dsk;
+    const SliceRange sr = slice_range(a.vocab, a.dslices, slice, P);
+    const S* rp = row + sr.v_begin;
+    const int64_t nelem = sr.v_end - sr.v_begin;
+    const uint4* vp = reinterpret_cast<const uint4*>(rp);
+    const int64_t last = max<int64_t>(nelem / P - 1, 0);
+    uint4 r[kWaveDepth], q[kWaveDepth];
+#pragma unroll
+    for (int u = 0; u < kWaveDepth; ++u) r[u] = load16_stream(vp + min<int64_t>(u * kWave + lane, last));
+#pragma unroll
+    for (int u = 0; u < kWaveDepth; ++u) q[u] = load16_stream(vp + min<int64_t>((kWaveDepth + u) * kWave + lane, last));
+    wave_scan_candidates<TagD>(ws, rp, nelem, sr.v_begin, f, p.top_k, r, q, count, raw_max, kth, ovf);
+    code = (ovf || count > kDraftCap) ? kPubBad : static_cast<uint64_t>(count);
+  }
+
+  // Publish this slice (plain stores: the resolve kernel, a later launch,
+  // merges the slices of the request).
+  uint64_t* pub = a.pub_d + b * kNBuf + static_cast<int64_t>(slice) * kDraftCap;
+  uint64_t* pubs = a.pubs_d + b * 2 * kDraftSlices;
+  if (code < kPubSkip)
+    for (int i = lane; i < count; i += kWave) pub[i] = ws.buf[i];
+  if (lane == 0) {
+    pubs[2 * slice] = code;
+    pubs[2 * slice + 1] = (static_cast<uint64_t>(ordered_f32(raw_max)) << 32) | ordered_f32(kth);
+  }
+}
+
+// Draft row of request b from its kDraftSlices published slices (one wave of
+// the resolve kernel): gathers the slices' candidates, keeps the row's k
+// largest and writes the row record and support.  The largest of the slices'
+// k-th values bounds the row's k-th largest from below, so only candidates
+// within the rounding margin of that bound are kept while gathering.  A slice
+// that could not decide the acceptance (or saw none rejected) leaves the row
+// to the exact pass unscanned; one whose candidates did not fit leaves it to
+// the exact pass with the row maximum.
+__device__ __forceinline__ void draft_merge_wave(const Args& a, WaveShared& ws, int64_t b, const Params& p) {
+  static_assert(kDraftSlices <= kWave, "one slice per lane");
+  const int lane = threadIdx.x & (kWave - 1);
+  const int ns = a.dslices;
+  const uint64_t* pubs = a.pubs_d + b * 2 * kDraftSlices;
+  uint64_t c = 0, mw = 0;
+  if (lane < ns) {
+    c = pubs[2 * lane];
+    mw = pubs[2 * lane + 1];
+  }
+  if (__ballot(lane < ns && c >= kPubSkip && c != kPubBad)) {
+    if (lane == 0) {
+      RowRec rr{};
+      rr.flags = kFlagOverflow | kFlagUnscanned;
+      rr.why = kWhyDefer;
+      a.rec_d[b] = rr;
+    }
+    return;
+  }
+  const float raw_max = wave_max(lane < ns ? unordered_f32(static_cast<uint32_t>(mw >> 32)) : -FLT_MAX);
+  const bool any_bad = __ballot(lane < ns && c == kPubBad) != 0;
+  int count = 0;
+  int merged_ovf = any_bad ? kWhyMerge : 0;
+  const XForm f{nullptr, nullptr, nullptr, 1.f, 0, nullptr};
+  if (!merged_ovf) {
+    const int cnt = lane < ns ? static_cast<int>(c) : 0;
+    // Two lanes per slice: lane l holds entries (l & 1) + 2t of slice l / 2
+    // (at most kDraftCap / 2 of them, all loaded at once; clamped to the
+    // slice's last entry, slot 0 or 1 of an empty slice).
+    constexpr int kPer = kDraftCap / 2;
+    const int sl = lane >> 1, par = lane & 1;
+    const int my_cnt = __shfl(cnt, sl, kWave);
+    const int my_n = (my_cnt - par + 1) >> 1;
+    const uint64_t* src = a.pub_d + b * kNBuf + static_cast<int64_t>(sl) * kDraftCap + par;
+    uint64_t v[kPer];
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) v[u] = src[2 * max(min(u, my_n - 1), 0)];
+    // Lower bound of the row's k-th largest: each lane's 4 largest entries
+    // are entries of the row, so the k-th largest of those 256 values (here
+    // its 16-bit ordered prefix, a value no larger) is no larger than the
+    // row's k-th largest; the slices' own k-th values bound it as well.
+    float t0 = -INFINITY, t1 = -INFINITY, t2 = -INFINITY, t3 = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      const float x = u < my_n ? key_s(v[u]) : -INFINITY;
+      t3 = __builtin_amdgcn_fmed3f(t2, t3, x);
+      t2 = __builtin_amdgcn_fmed3f(t1, t2, x);
+      t1 = __builtin_amdgcn_fmed3f(t0, t1, x);
+      t0 = fmaxf(t0, x);
+    }
+    const uint32_t o[4] = {ordered_f32(t0), ordered_f32(t1), ordered_f32(t2), ordered_f32(t3)};
+    // (-inf values among the 256 give a NaN prefix: no bound from them)
+    float lb = unordered_f32(wave_kth_ballot<4>(o, p.top_k, 16));
+    if (!(lb == lb)) lb = -INFINITY;
+    const float bound = fmaxf(lb, wave_max(lane < ns ? unordered_f32(static_cast<uint32_t>(mw)) : -INFINITY));
+    const uint32_t keep_from = bound > -INFINITY ? ordered_f32(x_lower(bound)) : 0u;
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      const bool keep = u < my_n && static_cast<uint32_t>(v[u] >> 32) >= keep_from;
+      const uint64_t m = __ballot(keep);
+      const int pos = count + __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
+                                                        __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u));
+      if (keep && pos < kWaveBuf) ws.buf[pos] = v[u];
+      count += __popcll(m);
+    }
+    wave_sync();
+    if (count > kWaveBuf) merged_ovf = kWhyMerge;
+    if (!merged_ovf) {
+      int ntrans = count;
+      wave_compact_topk(ws, f, count, ntrans, p.top_k, false);
+    }
+  }
+  wave_finalize_topk(ws, count, p, raw_max, merged_ovf, a.rec_d + b, a.sidx_d + b * kCap, a.sp_d + b * kCap, -1,
+                     NAN, a.list_cnt + 1, a.list_d, static_cast<int32_t>(b));
+}
+
+// Draft slices of a launch that runs after the target fallback.
+template <typename TagD, typename CandT>
+__global__ __launch_bounds__(kWave) void draft_wave_kernel(Args a) {
+  __shared__ WaveShared ws;
+  draft_wave_slice<TagD, CandT, false>(a, ws, blockIdx.x / a.dslices, blockIdx.x % a.dslices);
+}
+
+// One wavefront per target row that is top-k with k <= kWaveMaxK: stream the
+// row, keep its k largest transformed logits (within the margin) and write
+// the row record and support.  With a.fuse_draft the grid carries, after the
+// B*K target rows, a.dslices draft slices per request; each target row
+// then publishes its acceptance word, and the draft slices of a request start
+// as soon as the words up to the first rejection are published (workgroups
+// are dispatched in order on each XCD, so every target row is resident or
+// done before a draft slice of the same XCD waits).
+template <typename TagT, typename TagD, typename CandT>
+__global__ __launch_bounds__(kWave) void verify_wave_kernel(Args a) {
+  __shared__ WaveShared ws;
+  using S = typename TagT::storage;
+  constexpr int P = TagT::kPerVec;
+  const int64_t rows = a.batch * a.width;
+  if (static_cast<int64_t>(blockIdx.x) >= rows) {
+    const int64_t d = blockIdx.x - rows;
+    draft_wave_slice<TagD, CandT, true>(a, ws, d / a.dslices, static_cast<int>(d % a.dslices));
+    return;
+  }
+  const int64_t row = blockIdx.x;
+  const int64_t b = row / a.width;
+  const int lane = threadIdx.x;
+  const S* rp = static_cast<const S*>(a.logits) + row * a.lrs;
   const uint4* vp = reinterpret_cast<const uint4*>(rp);
-  const int64_t last = max<int64_t>(nelem / P - 1, 0);
+  const int64_t last = a.vocab / P - 1;
+  // The first two chunks are requested before the row's parameters are read,
+  // so their latency overlaps the set-up (a row of another path discards them).
   uint4 r[kWaveDepth], q[kWaveDepth];
 #pragma unroll
   for (int u = 0; u < kWaveDepth; ++u) r[u] = load16_stream(vp + min<int64_t>(u * kWave + lane, last));
 #pragma unroll
   for (int u = 0; u < kWaveDepth; ++u) q[u] = load16_stream(vp + min<int64_t>((kWaveDepth + u) * kWave + lane, last));
-  const XForm f{nullptr, nullptr, nullptr, 1.f, 0, nullptr};
-  int count, ovf;
-  float raw_max;
-  wave_scan_candidates<TagD>(ws, rp, nelem, sr.v_begin, f, p.top_k, r, q, count, raw_max, ovf);
-
-  // Publish this slice, arrive; the last slice gathers the row.
-  uint64_t* pub = a.pub_d + b * kNBuf + static_cast<int64_t>(slice) * kDraftCap;
-  uint64_t* pubs = a.pubs_d + b * 2 * kDraftSlices;
-  const bool bad = ovf || count > kDraftCap;
-  if (!bad)
-    for (int i = lane; i < count; i += kWave) atomic_put_u64(pub + i, ws.buf[i]);
-  int last_slice = 0;
-  if (lane == 0) {
-    atomic_put_u64(pubs + 2 * slice, bad ? ~uint64_t(0) : static_cast<uint64_t>(count));
-    atomic_put_u64(pubs + 2 * slice + 1, static_cast<uint64_t>(ordered_f32(raw_max)));
-    last_slice = arrive(a.cnt_d + b) == static_cast<uint32_t>(kDraftSlices - 1);
-  }
-  last_slice = __shfl(last_slice, 0, kWave);
-  if (!last_slice) return;
-  if (lane == 0) atomic_take_u32(a.cnt_d + b);
-  // lane s < kDraftSlices takes slice s's count and maximum
-  uint64_t c = 0;
-  float smx = -FLT_MAX;
-  if (lane < kDraftSlices) {
-    c = atomic_take_u64(pubs + 2 * lane);
-    smx = unordered_f32(static_cast<uint32_t>(atomic_take_u64(pubs + 2 * lane + 1)));
-  }
-  const bool any_bad = __ballot(lane < kDraftSlices && c == ~uint64_t(0)) != 0;
-  const int cnt = (lane < kDraftSlices && c != ~uint64_t(0)) ? static_cast<int>(c) : 0;
-  int total;
-  const int off = wave_excl_scan(cnt, &total);
-  raw_max = wave_max(smx);
-  int merged_ovf = (any_bad || total > kWaveBuf) ? kWhyMerge : 0;
-  if (!merged_ovf) {
-    for (int s2 = 0; s2 < kDraftSlices; ++s2) {
-      const int base = __shfl(off, s2, kWave), n2 = __shfl(cnt, s2, kWave);
-      const uint64_t* src = a.pub_d + b * kNBuf + static_cast<int64_t>(s2) * kDraftCap;
-      for (int i = lane; i < n2; i += kWave) ws.buf[base + i] = atomic_take_u64(const_cast<uint64_t*>(src) + i);
+  Params p{a.temps[b], a.top_ks ? max(a.top_ks[b], 1) : static_cast<int>(a.vocab), a.top_ps ? a.top_ps[b] : 1.f,
+           a.min_ps ? a.min_ps[b] : 0.f};
+  const XForm f = target_xform(a, b, row);
+  const int mode = row_mode(p, a.vocab);
+  const bool raw = mode == kModeTopK && raw_filter_ok(f, a.pnonpos, b);
+  uint64_t word = static_cast<uint64_t>(kFlagOverflow) << 32;  // acceptance not known in this launch
+  if (!(raw && p.top_k <= kWaveMaxK)) {
+    // Rows of the other paths.  In a raw-only launch the rows that are not raw
+    // go to the exact fallback unscanned; raw rows with larger k go there too
+    // when no workgroup raw scan follows.
+    if (((!raw && a.hint == kHintRawOnly) || (raw && a.wave_only)) && lane == 0) {
+      RowRec rr{};
+      rr.flags = kFlagOverflow | kFlagUnscanned;
+      rr.why = kWhyHint;
+      a.rec_t[row] = rr;
+      a.list_t[atomic_add_u32(a.list_cnt, 1u)] = static_cast<int32_t>(row);
     }
-    wave_sync();
-    int ntrans = total;
-    count = total;
-    wave_compact_topk(ws, f, count, ntrans, p.top_k, false);
+  } else {
+    const CandRec cr = a.cand_rec[row];
+    int count, ovf;
+    float raw_max;
+    float kth;
+    wave_scan_candidates<TagT>(ws, rp, a.vocab, 0, f, p.top_k, r, q, count, raw_max, kth, ovf);
+    word = wave_finalize_topk(ws, count, p, raw_max, ovf, a.rec_t + row, a.sidx_t + row * kCap, a.sp_t + row * kCap,
+                              cr.tok, cr.x, a.list_cnt, a.list_t, static_cast<int32_t>(row));
   }
-  wave_finalize_topk(ws, count, p, raw_max, merged_ovf, a.rec_d + b, a.sidx_d + b * kCap, a.sp_d + b * kCap, -1,
-                     NAN, a.list_cnt + 1, a.list_d, static_cast<int32_t>(b));
+  if (a.fuse_draft && lane == 0) atomic_put_u64(a.acc_t + row, word | kAccPublished);
 }
 
 // Exact support of the rows the scan kernels could not resolve from their
@@ -1937,33 +2119,22 @@ __global__ __launch_bounds__(kT) void target_fallback_kernel(Args a) {
   }
 }
 
-template <typename TagD, typename CandT>
-__global__ __launch_bounds__(kT) void draft_fallback_kernel(Args a) {
-  __shared__ Shared sh;
-  __shared__ int s_len, s_flags;
-  const uint32_t n = *(a.list_cnt + 1);
-  for (uint32_t li = blockIdx.x; li < n; li += gridDim.x) {
-    const int64_t b = a.list_d[li];
-    accept_length_block<CandT>(a, b, &s_len, &s_flags);
-    __syncthreads();
-    const int len = s_len;
-    const RowRec prev = a.rec_d[b];
-    Params p;
-    p.temperature = a.d_temps ? a.d_temps[b] : a.temps[b];
-    p.top_k = a.d_top_ks ? max(a.d_top_ks[b], 1) : static_cast<int>(a.vocab);
-    p.top_p = a.d_top_ps ? a.d_top_ps[b] : 1.f;
-    p.min_p = a.d_min_ps ? a.d_min_ps[b] : 0.f;
-    using S = typename TagD::storage;
-    const S* rp = static_cast<const S*>(a.draft) + b * a.dsb + static_cast<int64_t>(len) * a.dsk;
-    XForm f{nullptr, nullptr, nullptr, 1.f, 0, nullptr};
-    const int mode = row_mode(p, a.vocab);
-    float m_x = prev.m, z = prev.z;
-    if (prev.flags & kFlagUnscanned) row_stats<TagD>(sh, rp, a.vocab, f, p.temperature, &m_x, &z);
-    const Exact ex = exact_support<TagD>(sh, rp, a.vocab, f, p, mode, m_x, z);
-    const int n_f = ex.n <= kCap ? collect<TagD>(sh, rp, a.vocab, f, p.temperature, ex.kcut) : 0;
-    write_exact_record(sh, ex, n_f, a.rec_d + b, a.sidx_d + b * kCap, a.sp_d + b * kCap, -1, NAN, p.temperature,
-                       prev.why);
-  }
+// Exact support of request b's draft row at position len (a row the draft
+// scans could not resolve); rewrites its record and support.  Called by the
+// whole workgroup.
+template <typename TagD>
+__device__ __forceinline__ void draft_exact_pass(Shared& sh, const Args& a, int64_t b, int len, const RowRec prev) {
+  const Params p = draft_params(a, b);
+  using S = typename TagD::storage;
+  const S* rp = static_cast<const S*>(a.draft) + b * a.dsb + static_cast<int64_t>(len) * a.dsk;
+  XForm f{nullptr, nullptr, nullptr, 1.f, 0, nullptr};
+  const int mode = row_mode(p, a.vocab);
+  float m_x = prev.m, z = prev.z;
+  if (prev.flags & kFlagUnscanned) row_stats<TagD>(sh, rp, a.vocab, f, p.temperature, &m_x, &z);
+  const Exact ex = exact_support<TagD>(sh, rp, a.vocab, f, p, mode, m_x, z);
+  const int n_f = ex.n <= kCap ? collect<TagD>(sh, rp, a.vocab, f, p.temperature, ex.kcut) : 0;
+  write_exact_record(sh, ex, n_f, a.rec_d + b, a.sidx_d + b * kCap, a.sp_d + b * kCap, -1, NAN, p.temperature,
+                     prev.why);
 }
 
 // Probability of token v under the target row record (dense supports only).
@@ -2066,14 +2237,16 @@ __device__ int cdf_find(Shared& sh, int n, float u, F val, float total) {
 template <typename TagT, typename TagD, typename CandT>
 __global__ __launch_bounds__(kT) void resolve_kernel(Args a) {
   __shared__ Shared sh;
+  __shared__ WaveShared ws;
   __shared__ int s_len, s_flags, s_tok;
   __shared__ float s_mass, s_total;
   const int64_t b = blockIdx.x;
   const int tid = threadIdx.x;
-  if (b == 0 && tid == 0) {
+  if (tid == 0 && b == 0) {
     atomic_take_u32(a.list_cnt);
     atomic_take_u32(a.list_cnt + 1);
   }
+  if (a.fuse_draft && tid < a.width) atomic_take_u64(a.acc_t + b * a.width + tid);
   accept_length_block<CandT>(a, b, &s_len, &s_flags);
   __syncthreads();
   const int len = s_len;
@@ -2084,7 +2257,24 @@ __global__ __launch_bounds__(kT) void resolve_kernel(Args a) {
   const RowRec tr = a.rec_t[trow];
   const bool rejected = len < g;
   RowRec dr{};
-  if (rejected && a.q_mode == 0) dr = a.rec_d[b];
+  if (rejected && a.q_mode == 0 && !s_flags && !(tr.flags & kFlagOverflow)) {
+    if (a.dwave) {
+      const Params pd = draft_params(a, b);
+      if (row_mode(pd, a.vocab) == kModeTopK && pd.top_k <= kWaveMaxK) {
+        // a draft row of the wavefront slices: merge them
+        if (tid < kWave) draft_merge_wave(a, ws, b, pd);
+        __syncthreads();
+      }
+    }
+    dr = a.rec_d[b];
+    if (dr.flags & kFlagOverflow) {
+      // a draft row the scans left to the exact pass
+      draft_exact_pass<TagD>(sh, a, b, len, dr);
+      dr = a.rec_d[b];
+    }
+  } else if (rejected && a.q_mode == 0) {
+    dr = a.rec_d[b];
+  }
   const bool blocked = s_flags || (tr.flags & kFlagOverflow) ||
                        (rejected && a.q_mode == 0 && (dr.flags & (kFlagOverflow | kFlagSkip)));
   if (blocked) {
@@ -2182,11 +2372,9 @@ struct Layout {
 Layout layout(int64_t batch, int width, int64_t vocab, int max_top_k) {
   Layout l{};
   const int64_t rows = batch * width;
-  const char* tw = getenv("LS_TUNE_TARGET_WGS");
-  const char* dw = getenv("LS_TUNE_DRAFT_WGS");
-  l.s_t = pick_slices(rows, vocab, tw ? atoi(tw) : 2048, max_top_k);
-  l.s_d = pick_slices(batch, vocab, dw ? atoi(dw) : 1024, max_top_k);
-  l.counters = up256(4 * rows) + up256(4 * batch) + 256;
+  l.s_t = pick_slices(rows, vocab, 2048, max_top_k);
+  l.s_d = pick_slices(batch, vocab, 1024, max_top_k);
+  l.counters = up256(4 * rows) + up256(4 * batch) + 256 + up256(8 * rows);
   uint64_t o = 0;
   l.off_rec_t = o; o += up256(sizeof(RowRec) * rows);
   l.off_sidx_t = o; o += up256(4ull * rows * kCap);
@@ -2267,6 +2455,7 @@ extern "C" int ls_verify_sample(const ls_verify_sample_args* in, void* counters,
   a.cnt_t = reinterpret_cast<uint32_t*>(c);
   a.cnt_d = reinterpret_cast<uint32_t*>(c + up256(4 * rows));
   a.list_cnt = reinterpret_cast<uint32_t*>(c + up256(4 * rows) + up256(4 * x.batch));
+  a.acc_t = reinterpret_cast<uint64_t*>(c + up256(4 * rows) + up256(4 * x.batch) + 256);
   char* s = static_cast<char*>(scratch);
   a.rec_t = reinterpret_cast<RowRec*>(s + l.off_rec_t);
   a.sidx_t = reinterpret_cast<int32_t*>(s + l.off_sidx_t);
@@ -2284,12 +2473,11 @@ extern "C" int ls_verify_sample(const ls_verify_sample_args* in, void* counters,
   a.s_t = l.s_t;
   a.s_d = l.s_d;
   a.hint = x.scan_hint;
-  a.wave = a.wave_only = a.dwave = a.dwave_only = 0;
+  a.wave = a.wave_only = a.dwave = a.dwave_only = a.fuse_draft = 0;
   hipStream_t st = static_cast<hipStream_t>(stream);
 
   const dim3 g_t(static_cast<unsigned>(rows * l.s_t)), g_d(static_cast<unsigned>(x.batch * l.s_d)),
       g_r(static_cast<unsigned>(x.batch)), g_f(static_cast<unsigned>(rows < 256 ? rows : 256)),
-      g_fd(static_cast<unsigned>(x.batch < 256 ? x.batch : 256)),
       g_c(static_cast<unsigned>((rows + rs::kT - 1) / rs::kT));
   void* const* ev = x.timing_events;
 #define LS_EVENT(i)                                                                              \
@@ -2309,9 +2497,15 @@ extern "C" int ls_verify_sample(const ls_verify_sample_args* in, void* counters,
     LS_LAUNCH_CHECK();                                                                                        \
     a.wave = (a.hint != kHintExactOnly && tv && x.vocab / TT::kPerVec >= int64_t(kWave) * kWaveDepth) ? 1 : 0; \
     a.wave_only = (a.wave && x.max_top_k > 0 && x.max_top_k <= kWaveMaxRowK) ? 1 : 0;                          \
+    a.dslices = static_cast<int>(x.vocab / (TD::kPerVec * kWave * kWaveDepth) < kDraftSlices                  \
+                                     ? x.vocab / (TD::kPerVec * kWave * kWaveDepth) : kDraftSlices);          \
+    a.dwave = (x.q_mode == 0 && a.hint != kHintExactOnly && dv && a.dslices >= kDraftMinSlices) ? 1 : 0;      \
+    a.dwave_only = (a.dwave && x.max_top_k > 0 && x.max_top_k <= kWaveMaxRowK) ? 1 : 0;                       \
+    a.fuse_draft = (a.wave && a.dwave) ? 1 : 0;                                                               \
     if (ev) LS_EVENT(0);                                                                                      \
     if (a.wave) {                                                                                             \
-      target_wave_kernel<TT, CT><<<dim3(static_cast<unsigned>(rows)), kWave, 0, st>>>(a);                    \
+      const int64_t nwg = rows + (a.fuse_draft ? x.batch * a.dslices : 0);                                    \
+      verify_wave_kernel<TT, TD, CT><<<dim3(static_cast<unsigned>(nwg)), kWave, 0, st>>>(a);                 \
       LS_LAUNCH_CHECK();                                                                                      \
     }                                                                                                         \
     if (a.hint != kHintExactOnly && !a.wave_only) {                                                           \
@@ -2328,11 +2522,8 @@ extern "C" int ls_verify_sample(const ls_verify_sample_args* in, void* counters,
     target_fallback_kernel<TT, CT><<<g_f, rs::kT, 0, st>>>(a);                                                \
     LS_LAUNCH_CHECK();                                                                                        \
     if (x.q_mode == 0) {                                                                                      \
-      a.dwave = (a.hint != kHintExactOnly && dv &&                                                            \
-                 x.vocab / kDraftSlices / TD::kPerVec >= int64_t(kWave) * kWaveDepth) ? 1 : 0;               \
-      a.dwave_only = (a.dwave && x.max_top_k > 0 && x.max_top_k <= kWaveMaxRowK) ? 1 : 0;                     \
-      if (a.dwave) {                                                                                          \
-        draft_wave_kernel<TD, CT><<<dim3(static_cast<unsigned>(x.batch * kDraftSlices)), kWave, 0, st>>>(a);  \
+      if (a.dwave && !a.fuse_draft) {                                                                         \
+        draft_wave_kernel<TD, CT><<<dim3(static_cast<unsigned>(x.batch * a.dslices)), kWave, 0, st>>>(a);     \
         LS_LAUNCH_CHECK();                                                                                    \
       }                                                                                                       \
       if (a.hint != kHintExactOnly && !a.dwave_only) {                                                        \
@@ -2345,8 +2536,6 @@ extern "C" int ls_verify_sample(const ls_verify_sample_args* in, void* counters,
         else draft_scan_kernel<TD, false, CT, kPathExact><<<g_d, rs::kT, 0, st>>>(a);                        \
         LS_LAUNCH_CHECK();                                                                                    \
       }                                                                                                       \
-      draft_fallback_kernel<TD, CT><<<g_fd, rs::kT, 0, st>>>(a);                                              \
-      LS_LAUNCH_CHECK();                                                                                      \
     }                                                                                                         \
     if (ev) LS_EVENT(2);                                                                                      \
     resolve_kernel<TT, TD, CT><<<g_r, rs::kT, 0, st>>>(a);                                                    \

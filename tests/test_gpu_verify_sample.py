@@ -11,7 +11,9 @@ Workloads (full 151,936 vocabulary unless stated):
   * pure temperature (dense support), batch 4;
   * dense draft probabilities (q_mode 1), batch 4;
   * the verify-path penalty quirk;
-  * small vocabularies with heavy ties and top-k 1 / 5 / 50 / >= V.
+  * small vocabularies with heavy ties and top-k 1 / 5 / 50 / >= V;
+  * each scan-kernel choice (raw-only with and without max_top_k, exact
+    only), including rows that a raw-only launch sends to the fallback.
 Bit-exact accept lengths and tokens except near-ties (tests/verify_ref.py);
 drafted-token target probabilities within 1e-5 relative.
 """
@@ -25,7 +27,7 @@ from tests import verify_ref as vr
 pytestmark = pytest.mark.gpu
 
 
-def run_kernel(dev, d, *, verify_quirk=False, draft_params=True, dense_q=None):
+def run_kernel(dev, d, *, verify_quirk=False, draft_params=True, dense_q=None, scan_hint=0, max_top_k=None):
     p = d["params"]
     tables = None
     if "history" in d:
@@ -45,14 +47,15 @@ def run_kernel(dev, d, *, verify_quirk=False, draft_params=True, dense_q=None):
         temperatures=p.temperatures.to(dev), top_ks=p.top_ks.to(dev), top_ps=p.top_ps.to(dev),
         min_ps=p.min_ps.to(dev), uniforms=d["uniforms"].to(dev), final_uniforms=d["final_uniforms"].to(dev),
         penalties=tables, vocab_mask=d["vocab_mask"].to(dev) if "vocab_mask" in d else None,
-        return_p_cand=True, check=True, **kw)
+        return_p_cand=True, check=True, scan_hint=scan_hint, max_top_k=max_top_k, **kw)
     torch.cuda.synchronize()
     return acc.cpu(), bonus.cpu(), pc.cpu()
 
 
-def check_case(dev, d, *, verify_quirk=False, label=""):
-    print(f"verify_sample case {label}: B={d['candidates'].shape[0]} V={d['logits'].shape[1]}", flush=True)
-    acc, bonus, pc = run_kernel(dev, d, verify_quirk=verify_quirk)
+def check_case(dev, d, *, verify_quirk=False, label="", scan_hint=0, max_top_k=None):
+    print(f"verify_sample case {label}: B={d['candidates'].shape[0]} V={d['logits'].shape[1]} "
+          f"hint={scan_hint} max_top_k={max_top_k}", flush=True)
+    acc, bonus, pc = run_kernel(dev, d, verify_quirk=verify_quirk, scan_hint=scan_hint, max_top_k=max_top_k)
     c = vr.oracle_inputs(d, verify_quirk=verify_quirk)
     lens_r, bonus_r, probs_r = vr.run_oracle(c)
     bad, exempt, msgs = vr.classify(c, acc, bonus, lens_r, bonus_r, probs_r, pc)
@@ -79,6 +82,35 @@ def test_topk_repetition_history(dev):
     d = workloads.stochastic_inputs(16, 16, seed=13, temperature=0.7, top_k=50, top_p=0.95, history_len=2048,
                                     repetition=1.05)
     check_case(dev, d, label="k50 p0.95 rep1.05")
+
+
+@pytest.mark.parametrize("scan_hint,max_top_k", [(1, 50), (1, None), (2, None), (0, 50)])
+def test_scan_hints_topk(dev, scan_hint, max_top_k):
+    # (1, 50): raw-only launch in which the wavefront kernels take every row
+    # and the draft slices run inside the target launch; (1, None): the
+    # workgroup raw scans follow; (2, None): exact scans only.
+    d = workloads.stochastic_inputs(16, 16, seed=21, temperature=0.7, top_k=50, top_p=0.95, history_len=2048,
+                                    repetition=1.05)
+    check_case(dev, d, label="k50 p0.95 rep1.05", scan_hint=scan_hint, max_top_k=max_top_k)
+
+
+@pytest.mark.parametrize("scan_hint,max_top_k", [(1, 64), (0, 64)])
+def test_scan_hints_rows_off_the_raw_path(dev, scan_hint, max_top_k):
+    # A negative presence penalty takes every row off the raw-logit path: in a
+    # raw-only launch the target rows go to the exact fallback unscanned, the
+    # draft slices in the target launch cannot decide the acceptance and leave
+    # the draft rows to the exact pass of the resolve kernel.
+    d = workloads.stochastic_inputs(6, 16, seed=22, temperature=0.9, top_k=64, top_p=0.9, history_len=3000,
+                                    repetition=1.1, presence=-0.7, frequency=0.05)
+    check_case(dev, d, label="k64 negative presence", scan_hint=scan_hint, max_top_k=max_top_k)
+
+
+@pytest.mark.parametrize("scan_hint,max_top_k", [(1, 5), (2, None)])
+def test_scan_hints_small_vocab_ties(dev, scan_hint, max_top_k):
+    d = workloads.stochastic_inputs(6, 8, 2000, seed=23, temperature=1.0, top_k=5, top_p=0.8)
+    g = torch.Generator().manual_seed(5)
+    d["logits"] = torch.randint(-4, 5, d["logits"].shape, generator=g).to(torch.bfloat16)
+    check_case(dev, d, label="ties k=5", scan_hint=scan_hint, max_top_k=max_top_k)
 
 
 def test_topk_negative_presence_exact_loop(dev):
