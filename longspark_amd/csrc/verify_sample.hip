@@ -1554,15 +1554,75 @@ __device__ __forceinline__ void wave_scan_candidates(WaveShared& ws, const typen
 // transformed, at least the k largest within the margin): re-key by x / T,
 // sort, cut by top-k (ties to the lowest index), top-p and min-p, and write
 // the row record and support.  A row the candidates cannot resolve (ovf) is
-// listed for the exact fallback with its raw maximum.  Returns, in lane 0,
-// the row's acceptance word: flags << 32 | bits(p_cand).
-__device__ uint64_t wave_finalize_topk(WaveShared& ws, int count, const Params& p, float raw_max, int ovf, RowRec* rec,
+// listed for the exact fallback with its raw maximum.  Returns the record
+// (the same in every lane).
+__device__ RowRec wave_finalize_topk(WaveShared& ws, int count, const Params& p, float raw_max, int ovf, RowRec* rec,
                                    int32_t* sidx, float* sp, int cand_tok, float cand_x, uint32_t* list_cnt,
                                    int32_t* list, int32_t list_id) {
   const int lane = threadIdx.x & (kWave - 1);
   const int k = p.top_k;
   const float t = p.temperature;
   int n = count;
+  if (!ovf && n <= kWave) {
+    // One key per lane, kept in registers: the arithmetic (and its order) of
+    // the general path below, without its LDS round trips.
+    uint64_t key = 0;
+    if (lane < n) {
+      const uint64_t k0 = ws.buf[lane];
+      key = cand_key(key_s(k0) / t, key_idx(k0));
+    }
+#pragma unroll
+    for (int size = 2; size <= kWave; size <<= 1) {
+#pragma unroll
+      for (int stride = size >> 1; stride > 0; stride >>= 1) {
+        const uint64_t o = __shfl_xor(key, stride, kWave);
+        const bool desc = (lane & size) == 0 || size == kWave;
+        const bool lower = (lane & stride) == 0;
+        key = (lower == desc) ? (key > o ? key : o) : (key < o ? key : o);
+      }
+    }
+    wave_sync();
+    ws.buf[lane] = key;  // the sorted support keys stay in LDS for the caller
+    wave_sync();
+    if (n > k) n = k;
+    const float m = n > 0 ? key_s(__shfl(key, 0, kWave)) : -INFINITY;
+    const float e = lane < n ? __expf(key_s(key) - m) : 0.f;
+    const float z1 = wave_sum(e);
+    const float pi = lane < n ? e / z1 : 0.f;
+    int n_f = n;
+    if (p.top_p < 1.0f && n > 0) {
+      const float inc = wave_incl_scan_f(pi);
+      const uint64_t hit = __ballot(lane < n && 0.f + inc - pi > p.top_p);
+      if (hit) n_f = __ffsll(static_cast<long long>(hit)) - 1;
+    }
+    if (p.min_p > 0.f && n_f > 0) {
+      const float pp = wave_sum(lane < n_f ? pi : 0.f);
+      const float thr = (__shfl(pi, 0, kWave) / pp) * p.min_p;
+      const uint64_t hit = __ballot(lane < n_f && pi / pp < thr);
+      if (hit) n_f = __ffsll(static_cast<long long>(hit)) - 1;
+    }
+    const float zf = wave_sum(lane < n_f ? e : 0.f);
+    if (lane < n_f) {
+      sidx[lane] = key_idx(key);
+      sp[lane] = e / zf;
+    }
+    RowRec rr{};
+    rr.m = m;
+    rr.z = zf;
+    rr.n = n_f;
+    rr.flags = 0;
+    rr.why = 0;
+    const uint64_t lastk = __shfl(key, n_f > 0 ? n_f - 1 : 0, kWave);
+    rr.last = n_f > 0 ? lastk : ~uint64_t(0);
+    rr.p_cand = 0.f;
+    if (cand_tok >= 0) {
+      const float sc = cand_x / t;
+      const uint64_t kc = cand_key(sc, cand_tok);
+      rr.p_cand = (kc >= rr.last && rr.n != 0) ? __expf(sc - rr.m) / rr.z : 0.f;
+    }
+    if (lane == 0) *rec = rr;
+    return rr;
+  }
   float m = 0.f, zf = 0.f;
   int n_f = 0;
   if (!ovf) {
@@ -1632,41 +1692,37 @@ __device__ uint64_t wave_finalize_topk(WaveShared& ws, int count, const Params& 
     for (int i = lane; i < n_f; i += kWave) a3 += __expf(key_s(ws.buf[i]) - m);
     zf = wave_sum(a3);
   }
+  RowRec rr{};
   if (ovf) {
+    rr.m = raw_max;  // x-domain upper bound of the row maximum
+    rr.z = 0.f;
+    rr.flags = kFlagOverflow;
+    rr.why = ovf;
     if (lane == 0) {
-      RowRec rr{};
-      rr.m = raw_max;  // x-domain upper bound of the row maximum
-      rr.z = 0.f;
-      rr.flags = kFlagOverflow;
-      rr.why = ovf;
       *rec = rr;
       list[atomic_add_u32(list_cnt, 1u)] = list_id;
     }
-    return static_cast<uint64_t>(kFlagOverflow) << 32;
+    return rr;
   }
   for (int i = lane; i < n_f; i += kWave) {
     const uint64_t kk = ws.buf[i];
     sidx[i] = key_idx(kk);
     sp[i] = __expf(key_s(kk) - m) / zf;
   }
-  if (lane == 0) {
-    RowRec rr;
-    rr.m = m;
-    rr.z = zf;
-    rr.n = n_f;
-    rr.flags = 0;
-    rr.why = 0;
-    rr.last = n_f > 0 ? ws.buf[n_f - 1] : ~uint64_t(0);
-    rr.p_cand = 0.f;
-    if (cand_tok >= 0) {
-      const float sc = cand_x / t;
-      const uint64_t kc = cand_key(sc, cand_tok);
-      rr.p_cand = (kc >= rr.last && rr.n != 0) ? __expf(sc - rr.m) / rr.z : 0.f;
-    }
-    *rec = rr;
-    return __float_as_uint(rr.p_cand);
+  rr.m = m;
+  rr.z = zf;
+  rr.n = n_f;
+  rr.flags = 0;
+  rr.why = 0;
+  rr.last = n_f > 0 ? ws.buf[n_f - 1] : ~uint64_t(0);
+  rr.p_cand = 0.f;
+  if (cand_tok >= 0) {
+    const float sc = cand_x / t;
+    const uint64_t kc = cand_key(sc, cand_tok);
+    rr.p_cand = (kc >= rr.last && rr.n != 0) ? __expf(sc - rr.m) / rr.z : 0.f;
   }
-  return 0;
+  if (lane == 0) *rec = rr;
+  return rr;
 }
 
 template <typename TagT, bool kVec, typename CandT, int kPath>
@@ -1913,88 +1969,93 @@ __device__ __forceinline__ void draft_wave_slice(const Args& a, WaveShared& ws, 
   }
 }
 
-// Draft row of request b from its kDraftSlices published slices (one wave of
-// the resolve kernel): gathers the slices' candidates, keeps the row's k
-// largest and writes the row record and support.  The largest of the slices'
-// k-th values bounds the row's k-th largest from below, so only candidates
-// within the rounding margin of that bound are kept while gathering.  A slice
-// that could not decide the acceptance (or saw none rejected) leaves the row
-// to the exact pass unscanned; one whose candidates did not fit leaves it to
-// the exact pass with the row maximum.
-__device__ __forceinline__ void draft_merge_wave(const Args& a, WaveShared& ws, int64_t b, const Params& p) {
-  static_assert(kDraftSlices <= kWave, "one slice per lane");
-  const int lane = threadIdx.x & (kWave - 1);
-  const int ns = a.dslices;
-  const uint64_t* pubs = a.pubs_d + b * 2 * kDraftSlices;
-  uint64_t c = 0, mw = 0;
-  if (lane < ns) {
-    c = pubs[2 * lane];
-    mw = pubs[2 * lane + 1];
-  }
-  if (__ballot(lane < ns && c >= kPubSkip && c != kPubBad)) {
-    if (lane == 0) {
-      RowRec rr{};
-      rr.flags = kFlagOverflow | kFlagUnscanned;
-      rr.why = kWhyDefer;
-      a.rec_d[b] = rr;
-    }
-    return;
-  }
-  const float raw_max = wave_max(lane < ns ? unordered_f32(static_cast<uint32_t>(mw >> 32)) : -FLT_MAX);
-  const bool any_bad = __ballot(lane < ns && c == kPubBad) != 0;
-  int count = 0;
-  int merged_ovf = any_bad ? kWhyMerge : 0;
-  const XForm f{nullptr, nullptr, nullptr, 1.f, 0, nullptr};
-  if (!merged_ovf) {
-    const int cnt = lane < ns ? static_cast<int>(c) : 0;
-    // Two lanes per slice: lane l holds entries (l & 1) + 2t of slice l / 2
-    // (at most kDraftCap / 2 of them, all loaded at once; clamped to the
-    // slice's last entry, slot 0 or 1 of an empty slice).
-    constexpr int kPer = kDraftCap / 2;
-    const int sl = lane >> 1, par = lane & 1;
-    const int my_cnt = __shfl(cnt, sl, kWave);
-    const int my_n = (my_cnt - par + 1) >> 1;
-    const uint64_t* src = a.pub_d + b * kNBuf + static_cast<int64_t>(sl) * kDraftCap + par;
-    uint64_t v[kPer];
+// Draft slice hand-off state of the resolve workgroup.
+struct MergeShared {
+  int cnt[kDraftSlices];        // candidates of each slice (0 past the launch's slices)
+  float bound;                  // lower bound of the row's k-th largest
+  int wave_base[kT / kWave];    // each wave's first slot in the merged list
+  int count;                    // merged list length
+};
+
+// Draft row of request b from its published slices (every thread of the
+// resolve workgroup): eight lanes per slice read its candidates (all at
+// once); the k-th largest of the threads' 2 largest candidates (entries of
+// the row, so no larger than the row's k-th largest; only its top 16 bits
+// are found, which lowers it further) bounds the row's k-th largest from
+// below, and the candidates within the rounding margin of that bound (or of
+// the slices' own k-th values) are kept.  Wave 0 then keeps the row's k
+// largest and writes the row record and support; the record is returned in
+// wave 0.
+__device__ __forceinline__ RowRec draft_merge_block(const Args& a, WaveShared& ws, MergeShared& ms, int64_t b,
+                                                    const Params& p, float slice_bound, float raw_max) {
+  constexpr int kLanes = kT / kDraftSlices;
+  constexpr int kPer = kDraftCap / kLanes;
+  static_assert(kLanes * kDraftSlices == kT && kPer * kLanes == kDraftCap, "merge lane layout");
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wid = tid / kWave;
+  const int sl = tid / kLanes, part = tid % kLanes;
+  const int my_n = (ms.cnt[sl] - part + kLanes - 1) / kLanes;  // entries part + kLanes * t
+  const uint64_t* src = a.pub_d + b * kNBuf + static_cast<int64_t>(sl) * kDraftCap + part;
+  uint64_t v[kPer];
 #pragma unroll
-    for (int u = 0; u < kPer; ++u) v[u] = src[2 * max(min(u, my_n - 1), 0)];
-    // Lower bound of the row's k-th largest: each lane's 4 largest entries
-    // are entries of the row, so the k-th largest of those 256 values (here
-    // its 16-bit ordered prefix, a value no larger) is no larger than the
-    // row's k-th largest; the slices' own k-th values bound it as well.
-    float t0 = -INFINITY, t1 = -INFINITY, t2 = -INFINITY, t3 = -INFINITY;
+  for (int u = 0; u < kPer; ++u) v[u] = src[kLanes * max(min(u, my_n - 1), 0)];
+  float t0 = -INFINITY, t1 = -INFINITY;
 #pragma unroll
-    for (int u = 0; u < kPer; ++u) {
-      const float x = u < my_n ? key_s(v[u]) : -INFINITY;
-      t3 = __builtin_amdgcn_fmed3f(t2, t3, x);
-      t2 = __builtin_amdgcn_fmed3f(t1, t2, x);
-      t1 = __builtin_amdgcn_fmed3f(t0, t1, x);
-      t0 = fmaxf(t0, x);
-    }
-    const uint32_t o[4] = {ordered_f32(t0), ordered_f32(t1), ordered_f32(t2), ordered_f32(t3)};
-    // (-inf values among the 256 give a NaN prefix: no bound from them)
-    float lb = unordered_f32(wave_kth_ballot<4>(o, p.top_k, 16));
+  for (int u = 0; u < kPer; ++u) {
+    const float x = u < my_n ? key_s(v[u]) : -INFINITY;
+    t1 = __builtin_amdgcn_fmed3f(t0, t1, x);
+    t0 = fmaxf(t0, x);
+  }
+  ws.buf[2 * tid] = ordered_f32(t0);
+  ws.buf[2 * tid + 1] = ordered_f32(t1);
+  __syncthreads();
+  if (wid == 0) {
+    constexpr int kVals = 2 * kT / kWave;
+    uint32_t o[kVals];
+#pragma unroll
+    for (int j = 0; j < kVals; ++j) o[j] = static_cast<uint32_t>(ws.buf[j * kWave + lane]);
+    // (-inf values among them give a NaN prefix: no bound from them)
+    float lb = unordered_f32(wave_kth_ballot<kVals>(o, p.top_k, 16));
     if (!(lb == lb)) lb = -INFINITY;
-    const float bound = fmaxf(lb, wave_max(lane < ns ? unordered_f32(static_cast<uint32_t>(mw)) : -INFINITY));
-    const uint32_t keep_from = bound > -INFINITY ? ordered_f32(x_lower(bound)) : 0u;
+    if (lane == 0) ms.bound = lb;
+  }
+  __syncthreads();
+  const float bound = fmaxf(slice_bound, ms.bound);
+  const uint32_t keep_from = bound > -INFINITY ? ordered_f32(x_lower(bound)) : 0u;
+  int kept = 0;
 #pragma unroll
-    for (int u = 0; u < kPer; ++u) {
-      const bool keep = u < my_n && static_cast<uint32_t>(v[u] >> 32) >= keep_from;
-      const uint64_t m = __ballot(keep);
-      const int pos = count + __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
-                                                        __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u));
-      if (keep && pos < kWaveBuf) ws.buf[pos] = v[u];
-      count += __popcll(m);
-    }
-    wave_sync();
-    if (count > kWaveBuf) merged_ovf = kWhyMerge;
-    if (!merged_ovf) {
+  for (int u = 0; u < kPer; ++u)
+    kept += __popcll(__ballot(u < my_n && static_cast<uint32_t>(v[u] >> 32) >= keep_from));
+  if (lane == 0) ms.wave_base[wid] = kept;
+  __syncthreads();
+  int base = 0, count = 0;
+#pragma unroll
+  for (int w = 0; w < kT / kWave; ++w) {
+    base += w < wid ? ms.wave_base[w] : 0;
+    count += ms.wave_base[w];
+  }
+#pragma unroll
+  for (int u = 0; u < kPer; ++u) {
+    const bool keep = u < my_n && static_cast<uint32_t>(v[u] >> 32) >= keep_from;
+    const uint64_t m = __ballot(keep);
+    const int pos = base + __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
+                                                     __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u));
+    if (keep && pos < kWaveBuf) ws.buf[pos] = v[u];
+    base += __popcll(m);
+  }
+  __syncthreads();
+  RowRec rr{};
+  if (wid == 0) {
+    const int ovf = count > kWaveBuf ? kWhyMerge : 0;
+    if (!ovf && count > kWave) {
+      // more than a register sort holds: keep the k largest first
+      const XForm f{nullptr, nullptr, nullptr, 1.f, 0, nullptr};
       int ntrans = count;
       wave_compact_topk(ws, f, count, ntrans, p.top_k, false);
     }
+    rr = wave_finalize_topk(ws, count, p, raw_max, ovf, a.rec_d + b, a.sidx_d + b * kCap, a.sp_d + b * kCap, -1,
+                            NAN, a.list_cnt + 1, a.list_d, static_cast<int32_t>(b));
   }
-  wave_finalize_topk(ws, count, p, raw_max, merged_ovf, a.rec_d + b, a.sidx_d + b * kCap, a.sp_d + b * kCap, -1,
-                     NAN, a.list_cnt + 1, a.list_d, static_cast<int32_t>(b));
+  return rr;
 }
 
 // Draft slices of a launch that runs after the target fallback.
@@ -2059,8 +2120,10 @@ __global__ __launch_bounds__(kWave) void verify_wave_kernel(Args a) {
     float raw_max;
     float kth;
     wave_scan_candidates<TagT>(ws, rp, a.vocab, 0, f, p.top_k, r, q, count, raw_max, kth, ovf);
-    word = wave_finalize_topk(ws, count, p, raw_max, ovf, a.rec_t + row, a.sidx_t + row * kCap, a.sp_t + row * kCap,
-                              cr.tok, cr.x, a.list_cnt, a.list_t, static_cast<int32_t>(row));
+    const RowRec rr = wave_finalize_topk(ws, count, p, raw_max, ovf, a.rec_t + row, a.sidx_t + row * kCap,
+                                         a.sp_t + row * kCap, cr.tok, cr.x, a.list_cnt, a.list_t,
+                                         static_cast<int32_t>(row));
+    word = (static_cast<uint64_t>(static_cast<uint32_t>(rr.flags)) << 32) | __float_as_uint(rr.p_cand);
   }
   if (a.fuse_draft && lane == 0) atomic_put_u64(a.acc_t + row, word | kAccPublished);
 }
@@ -2234,46 +2297,248 @@ __device__ int cdf_find(Shared& sh, int n, float u, F val, float total) {
   return res;
 }
 
+// Accepted length of request b (one wave; width <= 64, so lane j holds
+// position j's record): lane 0 writes it and its blocking flag (the overflow
+// flag of the record at the accepted length), and the lane holding the
+// record at the accepted length writes it to *s_tr.
+template <typename CandT>
+__device__ __forceinline__ int resolve_accept_wave(const Args& a, int64_t b, int* s_len, int* s_flags,
+                                                   RowRec* s_tr, int* flags) {
+  const int g = a.width - 1;
+  const int lane = threadIdx.x & (kWave - 1);
+  RowRec r{};
+  float q = 0.f, uv = 0.f;
+  if (lane <= g) r = a.rec_t[b * a.width + lane];
+  if (lane < g) {
+    uv = a.uni[b * a.usb + lane];
+    if (a.q_mode == 0) {
+      q = a.dtp[b * a.dtp_sb + lane];
+    } else {
+      const int64_t c = cand_at<CandT>(a, b, lane);
+      q = (c >= 0 && c < a.vocab)
+              ? static_cast<const float*>(a.draft)[b * a.dsb + static_cast<int64_t>(lane) * a.dsk + c]
+              : 0.f;
+    }
+  }
+  const bool ok = lane < g && !(r.flags & kFlagOverflow) && uv * q < r.p_cand;
+  const uint64_t fail = __ballot(lane < g && !ok);
+  const int len = fail ? __ffsll(static_cast<long long>(fail)) - 1 : g;
+  const int fl = __shfl(r.flags, len, kWave) & kFlagOverflow;
+  if (lane == len) *s_tr = r;
+  if (lane == 0) {
+    *s_len = len;
+    *s_flags = fl;
+  }
+  *flags = fl;
+  return len;
+}
+
+// Final draw of request b when the target support at the accepted length and
+// the draft support (if a residual is needed) have at most 64 entries each
+// (one wave, one entry per lane): q of each target entry by matching indices,
+// the residual max(p - q, 0) when a draft token was rejected (p itself below
+// the residual-mass floor), then the first entry in index order whose running
+// sum exceeds u times the total (vocab - 1 when the total is zero).
+// ti / tp: lane i's target support entry (i < tr.n), loaded by the caller.
+template <typename TagD>
+__device__ __forceinline__ void resolve_wave(const Args& a, int64_t b, int len, bool rejected, const RowRec& tr,
+                                             const RowRec& dr, const uint64_t* dkeys, int ti, float tp) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int n = tr.n;
+  const float u = a.funi[b];
+  float val = tp;
+  if (rejected) {
+    float q = 0.f;
+    if (a.q_mode == 1) {
+      if (lane < n) q = static_cast<const float*>(a.draft)[b * a.dsb + static_cast<int64_t>(len) * a.dsk + ti];
+    } else {
+      const int dn = dr.n;
+      int di = -1;
+      float dp = 0.f;
+      if (lane < dn) {
+        if (dkeys) {
+          // the support keys the merge left in LDS (x / T, descending), with
+          // the probabilities it wrote recomputed the same way
+          const uint64_t kk = dkeys[lane];
+          di = key_idx(kk);
+          dp = __expf(key_s(kk) - dr.m) / dr.z;
+        } else {
+          di = a.sidx_d[b * kCap + lane];
+          dp = a.sp_d[b * kCap + lane];
+        }
+      }
+      for (int j = 0; j < dn; ++j) {
+        const int dj = __builtin_amdgcn_readlane(di, j);
+        const float pj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dp), j));
+        if (dj == ti) q = pj;
+      }
+    }
+    const float res = lane < n ? fmaxf(tp - q, 0.f) : 0.f;
+    // single-q acceptance falls back to p below 1e-8 (accept_sampling.py:332-340);
+    // dense-q chain sampling always uses the residual (reject_sampling.py:101-121)
+    if (a.q_mode == 1 || wave_sum(res) > 1e-8f) val = res;
+  }
+  // entries in ascending index order (bitonic sort across the wave)
+  uint64_t key = lane < n ? (static_cast<uint64_t>(static_cast<uint32_t>(ti)) << 32) | __float_as_uint(val)
+                          : ~uint64_t(0);
+#pragma unroll
+  for (int size = 2; size <= kWave; size <<= 1) {
+#pragma unroll
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      const uint64_t o = __shfl_xor(key, stride, kWave);
+      const bool asc = (lane & size) == 0 || size == kWave;
+      const bool lower = (lane & stride) == 0;
+      key = (lower == asc) ? (key < o ? key : o) : (key > o ? key : o);
+    }
+  }
+  const float v = lane < n ? __uint_as_float(static_cast<uint32_t>(key)) : 0.f;
+  const float inc = wave_incl_scan_f(v);
+  const float total = __shfl(inc, kWave - 1, kWave);
+  const uint64_t hit = __ballot(lane < n && inc > u * total);
+  const int idx = static_cast<int>(key >> 32);
+  const int first = hit ? __ffsll(static_cast<long long>(hit)) - 1 : 0;
+  const int at = __shfl(idx, first, kWave);
+  if (lane == 0) {
+    a.accept[b] = len;
+    a.bonus[b] = (total > 0.f && hit) ? at : static_cast<int>(a.vocab - 1);
+  }
+}
+
+// Wave 0 of the resolve kernel, after the accepted length and the draft
+// row's merge (merged: its record, or null when no merge ran): blocked
+// requests, and the final draw when both supports are small.  Returns true
+// when the request is finished (outputs written); the workgroup path takes
+// the rest.
+template <typename TagD>
+__device__ __forceinline__ bool resolve_finish(const Args& a, const WaveShared& ws, int64_t b, int len, int fl,
+                                               const RowRec& tr, const RowRec* merged, int ti, float tp) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const bool rejected = len < a.width - 1;
+  RowRec dr{};
+  const uint64_t* dkeys = nullptr;
+  if (rejected && a.q_mode == 0 && !fl && !(tr.flags & kFlagOverflow)) {
+    if (merged) {
+      dr = *merged;
+      dkeys = ws.buf;
+    } else {
+      dr = a.rec_d[b];
+    }
+    if (dr.flags & kFlagOverflow) return false;  // the exact pass
+  } else if (rejected && a.q_mode == 0) {
+    dr = a.rec_d[b];
+  }
+  const bool blocked = fl || (tr.flags & kFlagOverflow) ||
+                       (rejected && a.q_mode == 0 && (dr.flags & (kFlagOverflow | kFlagSkip)));
+  if (blocked) {
+    if (lane == 0) {
+      a.accept[b] = -1;
+      a.bonus[b] = -1;
+      if (a.status) atomicOr(a.status, kFlagOverflow);
+    }
+    return true;
+  }
+  if (!(tr.n >= 0 && tr.n <= kWave &&
+        (!rejected || a.q_mode == 1 || (!(dr.flags & kFlagDense) && dr.n <= kWave))))
+    return false;
+  resolve_wave<TagD>(a, b, len, rejected, tr, dr, dkeys, ti, tp);
+  return true;
+}
+
 template <typename TagT, typename TagD, typename CandT>
 __global__ __launch_bounds__(kT) void resolve_kernel(Args a) {
   __shared__ Shared sh;
   __shared__ WaveShared ws;
-  __shared__ int s_len, s_flags, s_tok;
-  __shared__ float s_mass, s_total;
+  __shared__ MergeShared ms;
+  __shared__ int s_len, s_flags, s_merge, s_done;
+  __shared__ float s_sbound, s_rawmax;
+  __shared__ RowRec s_tr;
   const int64_t b = blockIdx.x;
   const int tid = threadIdx.x;
+  const int g = a.width - 1;
   if (tid == 0 && b == 0) {
     atomic_take_u32(a.list_cnt);
     atomic_take_u32(a.list_cnt + 1);
   }
   if (a.fuse_draft && tid < a.width) atomic_take_u64(a.acc_t + b * a.width + tid);
-  accept_length_block<CandT>(a, b, &s_len, &s_flags);
-  __syncthreads();
-  const int len = s_len;
-  const int g = a.width - 1;
   if (a.p_cand_out)
     for (int j = tid; j < g; j += kT) a.p_cand_out[b * g + j] = a.rec_t[b * a.width + j].p_cand;
-  const int64_t trow = b * a.width + len;
-  const RowRec tr = a.rec_t[trow];
-  const bool rejected = len < g;
-  RowRec dr{};
-  if (rejected && a.q_mode == 0 && !s_flags && !(tr.flags & kFlagOverflow)) {
-    if (a.dwave) {
+  // Wave 0: the accepted length, and whether the draft row at the rejection
+  // is merged from wavefront slices (1), listed bad by a slice (2), or not;
+  // the target support at the accepted length is requested meanwhile.
+  int ti = 0;
+  float tp = 0.f;
+  if (tid < kWave) {
+    const int lane = tid;
+    const int ns = a.dslices;
+    uint64_t c = 0, mw = 0;  // the slices' codes do not depend on the acceptance: requested first
+    if (a.q_mode == 0 && a.dwave && lane < ns) {
+      const uint64_t* pubs = a.pubs_d + b * 2 * kDraftSlices;
+      c = pubs[2 * lane];
+      mw = pubs[2 * lane + 1];
+    }
+    int fl;
+    const int len = resolve_accept_wave<CandT>(a, b, &s_len, &s_flags, &s_tr, &fl);
+    wave_sync();
+    const RowRec tr = s_tr;
+    if (lane < tr.n) {
+      const int64_t trow = b * a.width + len;
+      ti = a.sidx_t[trow * kCap + lane];
+      tp = a.sp_t[trow * kCap + lane];
+    }
+    int merge = 0;
+    if (len < g && a.q_mode == 0 && !fl && !(tr.flags & kFlagOverflow) && a.dwave) {
       const Params pd = draft_params(a, b);
       if (row_mode(pd, a.vocab) == kModeTopK && pd.top_k <= kWaveMaxK) {
-        // a draft row of the wavefront slices: merge them
-        if (tid < kWave) draft_merge_wave(a, ws, b, pd);
-        __syncthreads();
+        if (__ballot(lane < ns && c >= kPubSkip && c != kPubBad)) {
+          // a slice could not decide the acceptance: the exact pass, unscanned
+          if (lane == 0) {
+            RowRec rr{};
+            rr.flags = kFlagOverflow | kFlagUnscanned;
+            rr.why = kWhyDefer;
+            a.rec_d[b] = rr;
+          }
+        } else {
+          merge = __ballot(lane < ns && c == kPubBad) ? 2 : 1;
+          if (lane < kDraftSlices) ms.cnt[lane] = (lane < ns && c != kPubBad) ? static_cast<int>(c) : 0;
+          const float rmx = wave_max(lane < ns ? unordered_f32(static_cast<uint32_t>(mw >> 32)) : -FLT_MAX);
+          const float sb = wave_max(lane < ns ? unordered_f32(static_cast<uint32_t>(mw)) : -INFINITY);
+          if (lane == 0) {
+            s_rawmax = rmx;
+            s_sbound = sb;
+          }
+        }
       }
     }
+    if (lane == 0) s_merge = merge;
+  }
+  __syncthreads();
+  RowRec dm{};  // the merged draft record (wave 0)
+  const int merge = s_merge;
+  if (merge == 1) {
+    dm = draft_merge_block(a, ws, ms, b, draft_params(a, b), s_sbound, s_rawmax);
+  } else if (merge == 2 && tid < kWave) {
+    dm = wave_finalize_topk(ws, 0, draft_params(a, b), s_rawmax, kWhyMerge, a.rec_d + b, a.sidx_d + b * kCap,
+                            a.sp_d + b * kCap, -1, NAN, a.list_cnt + 1, a.list_d, static_cast<int32_t>(b));
+  }
+  if (tid < kWave) {
+    const bool done = resolve_finish<TagD>(a, ws, b, s_len, s_flags, s_tr, merge ? &dm : nullptr, ti, tp);
+    if (tid == 0) s_done = done ? 1 : 0;
+  }
+  __syncthreads();
+  if (s_done) return;
+  // Workgroup path: large or dense supports and rows for the exact pass.
+  const int len = s_len;
+  const int64_t trow = b * a.width + len;
+  const RowRec tr = s_tr;
+  const bool rejected = len < g;
+  RowRec dr{};
+  if (rejected && a.q_mode == 0) {
     dr = a.rec_d[b];
-    if (dr.flags & kFlagOverflow) {
+    if ((dr.flags & kFlagOverflow) && !s_flags && !(tr.flags & kFlagOverflow)) {
       // a draft row the scans left to the exact pass
       draft_exact_pass<TagD>(sh, a, b, len, dr);
       dr = a.rec_d[b];
     }
-  } else if (rejected && a.q_mode == 0) {
-    dr = a.rec_d[b];
   }
   const bool blocked = s_flags || (tr.flags & kFlagOverflow) ||
                        (rejected && a.q_mode == 0 && (dr.flags & (kFlagOverflow | kFlagSkip)));
@@ -2345,7 +2610,6 @@ __global__ __launch_bounds__(kT) void resolve_kernel(Args a) {
     a.accept[b] = len;
     a.bonus[b] = tok;
   }
-  (void)s_tok; (void)s_mass; (void)s_total;
 }
 
 inline uint64_t up256(uint64_t x) { return (x + 255) & ~uint64_t(255); }
