@@ -36,7 +36,7 @@ V = 151936
 # copy (x2.0 and x1.0).  The commands and raw counter values are in the
 # profiles/ summary named beside each figure.
 TRAFFIC = {
-    "target_scan_kernel": (679_048_173, "profiles/target_scan_kernel_verify_sample_B128_K16_V151936.md"),
+    "verify_wave_kernel": (726_954_702, "profiles/verify_wave_kernel_verify_sample_B128_K16_V151936.md"),
     "greedy_verify_kernel": (622_640_864, "profiles/greedy_verify_kernel_B128_K16_V151936.md"),
     "window_gather_kernel": (604_246_324, "profiles/window_gather_kernel_B8_L36_Hkv8_D128_ctx131072.md"),
     "summary_kernel": (646_838_203, "profiles/summary_kernel_B8_L36_R256_W16.md"),
@@ -115,7 +115,12 @@ class GreedyVerify:
 
 class HipEvents:
     """hipEvent_t handles from the HIP runtime (for timing kernels that one C ABI
-    call launches back to back on a stream)."""
+    call launches back to back on a stream).  The events are created for timing
+    only (hipEventDisableSystemFence): recording one then costs no cache
+    writeback, which would otherwise add a gap of several microseconds to the
+    stream at every event."""
+
+    DISABLE_SYSTEM_FENCE = 0x20000000
 
     def __init__(self, n):
         import ctypes
@@ -127,7 +132,7 @@ class HipEvents:
         self.handles = (ctypes.c_void_p * n)()
         for i in range(n):
             h = ctypes.c_void_p()
-            if self.hip.hipEventCreateWithFlags(ctypes.byref(h), 0) != 0:
+            if self.hip.hipEventCreateWithFlags(ctypes.byref(h), self.DISABLE_SYSTEM_FENCE) != 0:
                 raise RuntimeError("hipEventCreateWithFlags failed")
             self.handles[i] = h
 
@@ -156,13 +161,23 @@ class StochasticVerify:
         self.cfg = dict(temperature=0.7, top_k=50, top_p=0.95, history_len=2048, repetition=1.05)
         self.d = workloads.stochastic_inputs(batch, width, vocab, seed=2025, device=dev, gen_device=dev, **self.cfg)
         self.rows = batch * width
-        self.kernel = "target_scan_kernel"
-        self.kernel_bytes = self.rows * vocab * 2          # every target logit once
+        # The dominant kernel scans every target row and, in the same launch, the
+        # fp32 draft row at the rejection of every request that rejects a token.
+        self.kernel = "verify_wave_kernel"
+        self.kernel_bytes = None                            # set by count_rejected()
         # whole verify, as counted for the workload: logits + one fp32 draft row per
         # request + the int32 history
-        self.bytes = self.kernel_bytes + batch * vocab * 4 + batch * self.cfg["history_len"] * 4
+        self.bytes = self.rows * vocab * 2 + batch * vocab * 4 + batch * self.cfg["history_len"] * 4
         self.events = None
         self.step_idx = 0
+
+    def count_rejected(self, out):
+        """Algorithmic bytes of the dominant kernel for this input: every target
+        logit once, plus the draft row of each request that rejects."""
+        accept = out[0]
+        rejected = int((accept < self.width - 1).sum().item())
+        self.rejected = rejected
+        self.kernel_bytes = self.rows * self.vocab * 2 + rejected * self.vocab * 4
 
     def arm_timing(self, steps):
         self.events = HipEvents(4 * steps)
@@ -187,14 +202,15 @@ class StochasticVerify:
         n = self.step_idx
         e = self.events
         scan = sum(e.elapsed_ms(4 * i, 4 * i + 1) for i in range(n)) / n
-        draft = sum(e.elapsed_ms(4 * i + 1, 4 * i + 2) for i in range(n)) / n
+        fallback = sum(e.elapsed_ms(4 * i + 1, 4 * i + 2) for i in range(n)) / n
         resolve = sum(e.elapsed_ms(4 * i + 2, 4 * i + 3) for i in range(n)) / n
-        return {"target_scan_kernel": scan, "fallback+draft_scan_kernels": draft, "resolve_kernel": resolve}
+        return {"verify_wave_kernel": scan, "target_fallback_kernel": fallback, "resolve_kernel": resolve}
 
     def config(self):
         return {"workload": f"fused stochastic verify B={self.batch} K={self.width} V={self.vocab} bf16, T 0.7, "
                             "top-k 50, top-p 0.95, repetition 1.05 over a 2048-token Zipf history; draft rows fp32",
-                "batch": self.batch, "block": self.width, "vocab": self.vocab}
+                "batch": self.batch, "block": self.width, "vocab": self.vocab,
+                "rejecting_requests": getattr(self, "rejected", None)}
 
     def cpu_baseline(self, threads):
         from oracle import verify as ov
@@ -396,9 +412,12 @@ def main(argv=None):
     wl = WORKLOADS[args.workload](dev)
     stream = torch.cuda.current_stream(dev)
 
+    out = None
     for _ in range(args.warmup):
-        wl.step()
+        out = wl.step()
     torch.cuda.synchronize()
+    if hasattr(wl, "count_rejected"):
+        wl.count_rejected(out if out is not None else wl.step())
     if hasattr(wl, "arm_timing"):
         wl.arm_timing(args.steps)
     start = torch.cuda.Event(enable_timing=True)

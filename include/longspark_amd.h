@@ -189,8 +189,8 @@ LS_API int ls_adjust_logits(void* logits, int32_t logits_dtype, int64_t row_stri
  *   the token drawn from the residual (rejection) or from the last row (all
  *   accepted); p_cand_out [batch, width-1] (may be NULL) the target
  *   probability of each drafted token.  A request whose support exceeds the
- *   kernel's candidate capacity gets accept = bonus = -1 and ORs 1 into
- *   *status (may be NULL).
+ *   kernel's candidate capacity gets accept = bonus = -1 and sets *status
+ *   (may be NULL) to 1; the call clears *status first (on the stream).
  * ------------------------------------------------------------------------- */
 typedef struct {
   const void* logits;

@@ -1152,6 +1152,7 @@ __device__ __forceinline__ XForm target_xform(const Args& a, int64_t b, int64_t 
 template <typename TagT, typename CandT>
 __global__ __launch_bounds__(kT) void cand_prep_kernel(Args a) {
   const int64_t row = static_cast<int64_t>(blockIdx.x) * kT + threadIdx.x;
+  if (row == 0 && a.status) *a.status = 0;  // the first launch of the call clears the status word
   if (row >= a.batch * a.width) return;
   const int64_t b = row / a.width;
   const int j = static_cast<int>(row % a.width);

@@ -338,7 +338,7 @@ def verify_sample(*, logits: torch.Tensor, candidates: torch.Tensor, width: int,
     accept = torch.empty(batch, dtype=torch.int32, device=dev)
     bonus = torch.empty(batch, dtype=torch.int64, device=dev)
     p_cand = torch.empty(batch, g, dtype=torch.float32, device=dev) if return_p_cand else None
-    status = torch.zeros(1, dtype=torch.int32, device=dev)
+    status = torch.empty(1, dtype=torch.int32, device=dev)  # cleared by the call's first kernel
     a = _lib.VerifySampleArgs()
     a.logits, a.logits_dtype, a.logits_row_stride = logits.data_ptr(), _lib.dtype_code(logits), logits.stride(0)
     a.candidates, a.candidates_dtype = candidates.data_ptr(), _lib.dtype_code(candidates)

@@ -8,7 +8,8 @@ below are relative to the reference root; ``SRT`` abbreviates
 
 Tie rules adopted where the reference leaves them to a closed binary or to an
 unstable sort (parity against sgl-kernel / flashinfer is unpinned; these
-rules are pinned by brute force in tests/test_oracle_verify.py):
+rules are pinned by brute force in tests/test_oracle_greedy.py and
+tests/test_oracle_sampling.py):
   * argmax: first maximal index (documented torch.argmax behaviour).
   * top-k: the k largest scaled logits, ties at the k-th value broken towards
     the lowest vocabulary index (the order CUDA torch.topk gathers ties in).
@@ -27,7 +28,7 @@ RESIDUAL_MASS_EPS = 1e-8
 
 
 # --------------------------------------------------------------------------
-# a1: greedy verification
+# greedy verification
 # --------------------------------------------------------------------------
 
 def greedy_truth(target_logits: torch.Tensor) -> torch.Tensor:
@@ -74,7 +75,7 @@ def greedy_verify_split(drafted: torch.Tensor, logits: torch.Tensor):
 
 
 # --------------------------------------------------------------------------
-# a2 / a3: split-engine two-phase rejection sampling
+# split-engine two-phase rejection sampling
 # --------------------------------------------------------------------------
 
 @dataclass
@@ -153,7 +154,7 @@ def sample_rows_from_probs(probs: torch.Tensor, uniforms: torch.Tensor) -> torch
 
 
 # --------------------------------------------------------------------------
-# a7 / a8: penalties and vocabulary bitmask
+# penalties and vocabulary bitmask
 # --------------------------------------------------------------------------
 
 def penalty_tables(history, vocab: int, repetition, presence, frequency):
@@ -254,7 +255,7 @@ def apply_verify_adjustments(logits, *, additive=None, scaling=None, bitmask=Non
 
 
 # --------------------------------------------------------------------------
-# a6: target distribution (temperature, top-k, top-p, min-p)
+# target distribution (temperature, top-k, top-p, min-p)
 # --------------------------------------------------------------------------
 
 def stable_topk(x: torch.Tensor, k: int):
@@ -304,9 +305,9 @@ def target_probs(logits: torch.Tensor, *, temperatures, top_ks, top_ps, min_ps,
     ``scaled = logits / T``; if any request's top-k is below V, the sparse
     exact top-k-first path: top-k (tie rule above) with per-row masking of
     ranks >= k_row, softmax over the kept logits, top-p renorm, scatter to
-    dense zeros; otherwise dense softmax and top-p renorm.  Min-p (SURVEY M5:
-    absent from the reference verify path) follows the sampler order: after
-    top-k/top-p, ``SRT/layers/sampler.py:238-242``.
+    dense zeros; otherwise dense softmax and top-p renorm.  Min-p (absent from
+    the reference verify path) follows the sampler order: after top-k/top-p,
+    ``SRT/layers/sampler.py:238-242``.
     Per-request parameters are ``[B]`` tensors; ``top_k >= V`` disables top-k,
     ``top_p >= 1`` disables top-p and ``min_p <= 0`` disables min-p.
     """
@@ -339,7 +340,7 @@ def target_probs(logits: torch.Tensor, *, temperatures, top_ks, top_ps, min_ps,
 
 
 # --------------------------------------------------------------------------
-# a4: single-q acceptance with residual resampling (the fused-verify semantics)
+# single-q acceptance with residual resampling (the fused-verify semantics)
 # --------------------------------------------------------------------------
 
 def accept_single_q(*, candidates, target_probs_3d, draft_q_rows_fn, draft_token_probs,
@@ -387,7 +388,7 @@ def draft_q_rows(corrected_logits, positions, *, temperatures, top_ks=None, top_
 
 
 # --------------------------------------------------------------------------
-# a5: dense-q chain rejection sampling
+# dense-q chain rejection sampling
 # --------------------------------------------------------------------------
 
 def chain_speculative_sampling(*, candidates, uniform_samples, uniform_final, target_probs_3d,
