@@ -1519,22 +1519,42 @@ __device__ __forceinline__ void wave_scan_candidates(WaveShared& ws, const typen
       }                                                                     \
     }                                                                       \
   } while (0)
+// A chunk whose every vector lies inside the range: no bounds checks.
+#define LS_WAVE_CONSUME_FULL(BUF, S0)                                       \
+  do {                                                                      \
+    _Pragma("unroll") for (int u = 0; u < kWaveDepth; ++u) {                \
+      float x[P];                                                           \
+      unpack16<TagT>(BUF[u], x);                                            \
+      float vmax = x[0];                                                    \
+      _Pragma("unroll") for (int qq = 1; qq < P; ++qq) vmax = fmaxf(vmax, x[qq]); \
+      raw_max = fmaxf(raw_max, vmax);                                       \
+      if (__ballot(vmax >= tau))                                            \
+        wave_append<P>(ws, count, x, tau, e_off + (((S0) + u) * kWave + lane) * P); \
+    }                                                                       \
+  } while (0)
+#define LS_WAVE_CONSUME_ANY(BUF, S0)                                        \
+  do {                                                                      \
+    if (((S0) + kWaveDepth) * kWave <= nfull) LS_WAVE_CONSUME_FULL(BUF, S0); \
+    else LS_WAVE_CONSUME(BUF, S0);                                          \
+  } while (0)
 #define LS_WAVE_ISSUE(BUF, S0)                                              \
   do {                                                                      \
     _Pragma("unroll") for (int u = 0; u < kWaveDepth; ++u)                  \
       BUF[u] = load16_stream(vp + min<int64_t>(((S0) + u) * kWave + lane, last)); \
   } while (0)
-  LS_WAVE_CONSUME(r, 0);  // chunk 0 (read by the prologue); chunk 1 is in q
+  LS_WAVE_CONSUME_ANY(r, 0);  // chunk 0 (read by the prologue); chunk 1 is in q
   for (int64_t s0 = kWaveDepth; s0 < steps; s0 += 2 * kWaveDepth) {
     LS_WAVE_ISSUE(r, s0 + kWaveDepth);
     LS_WAVE_BOUNDARY();
-    LS_WAVE_CONSUME(q, s0);
+    LS_WAVE_CONSUME_ANY(q, s0);
     if (s0 + kWaveDepth >= steps) break;
     LS_WAVE_ISSUE(q, s0 + 2 * kWaveDepth);
     LS_WAVE_BOUNDARY();
-    LS_WAVE_CONSUME(r, s0 + kWaveDepth);
+    LS_WAVE_CONSUME_ANY(r, s0 + kWaveDepth);
   }
 #undef LS_WAVE_ISSUE
+#undef LS_WAVE_CONSUME_ANY
+#undef LS_WAVE_CONSUME_FULL
 #undef LS_WAVE_CONSUME
 #undef LS_WAVE_BOUNDARY
   // Elements past the last whole vector (range length not a multiple of P).
@@ -2085,7 +2105,10 @@ __global__ __launch_bounds__(kWave) void verify_wave_kernel(Args a) {
     draft_wave_slice<TagD, CandT, true>(a, ws, d / a.dslices, static_cast<int>(d % a.dslices));
     return;
   }
-  const int64_t row = blockIdx.x;
+  // Rows in position-major order: the first positions, which decide most
+  // requests' acceptance (and so when their draft rows can be scanned), are
+  // dispatched first.
+  const int64_t row = (blockIdx.x % a.batch) * a.width + blockIdx.x / a.batch;
   const int64_t b = row / a.width;
   const int lane = threadIdx.x;
   const S* rp = static_cast<const S*>(a.logits) + row * a.lrs;
