@@ -357,6 +357,88 @@ class SummaryUpdate:
                           f"median of {n} runs"}
 
 
+class SoftmaxTempWorkload:
+    """SoftmaxTemp.execute: fp32 softmax(logits / T) of B x K rows of 151,936
+    bf16 logits, batch 128 x block 16 (one temperature per request)."""
+
+    name = "softmax_temp"
+    metric = "temperature softmax GB/s (algorithmic bytes) at 128x16x151936, bf16 in, fp32 out"
+    unit = "GB/s"
+    dtype = "f32"
+
+    def __init__(self, dev, batch=128, width=16, vocab=V):
+        from longspark_amd import workloads
+        self.batch, self.width, self.vocab = batch, width, vocab
+        self.logits, _ = workloads.greedy_inputs(batch, width, vocab, seed=71, device=dev, gen_device=dev)
+        self.temps = torch.linspace(0.5, 1.5, batch, device=dev)
+        rows = batch * width
+        self.bytes = rows * vocab * 2 + rows * vocab * 4   # read the logits once, write the probabilities once
+        self.units = self.bytes / 1e9
+        self.kernel = "softmax_temp_kernel"
+
+    def step(self):
+        from longspark_amd import dense
+        return dense.softmax_temp(logits=self.logits, temperatures=self.temps, rows_per_request=self.width)
+
+    def config(self):
+        return {"workload": f"SoftmaxTemp B={self.batch} K={self.width} V={self.vocab} bf16 -> fp32",
+                "batch": self.batch, "block": self.width, "vocab": self.vocab}
+
+    def cpu_baseline(self, threads):
+        from oracle import verify as ov
+        torch.set_num_threads(threads)
+        rows = 32
+        x = self.logits[:rows].cpu()
+        t = self.temps[:rows // self.width].cpu()
+        med, n = time_cpu(lambda: ov.softmax_temp(x, t, self.width))
+        return {"value": rows * self.vocab * 6 / med / 1e9, "threads": threads,
+                "sample": f"{rows} rows x {self.vocab}, oracle torch-CPU softmax, median of {n} runs"}
+
+
+class TargetProbsWorkload:
+    """build_dflash_verify_target_probs: dense fp32 top-k 50 / top-p 0.95
+    distribution (T 0.7) of B x K rows of 151,936 bf16 logits, 128 x 16."""
+
+    name = "target_probs"
+    metric = "dense target distribution GB/s (algorithmic bytes) at 128x16x151936, top-k 50, top-p 0.95"
+    unit = "GB/s"
+    dtype = "f32"
+
+    def __init__(self, dev, batch=128, width=16, vocab=V):
+        from longspark_amd import workloads
+        self.batch, self.width, self.vocab = batch, width, vocab
+        self.logits, _ = workloads.greedy_inputs(batch, width, vocab, seed=72, device=dev, gen_device=dev)
+        self.params = workloads.SamplingParams.uniform(batch, temperature=0.7, top_k=50, top_p=0.95, device=dev)
+        rows = batch * width
+        self.bytes = rows * vocab * 2 + rows * vocab * 4   # read the logits once, write the dense rows once
+        self.units = self.bytes / 1e9
+        self.kernel = "ls_target_probs (all kernels of the call)"
+
+    def step(self):
+        from longspark_amd import dense
+        p = self.params
+        return dense.target_probs(logits=self.logits, temperatures=p.temperatures, rows_per_request=self.width,
+                                  top_ks=p.top_ks, top_ps=p.top_ps, max_top_k=50, scan_hint=1)
+
+    def config(self):
+        return {"workload": f"dense target probabilities B={self.batch} K={self.width} V={self.vocab} bf16 -> "
+                            "fp32, T 0.7, top-k 50, top-p 0.95", "batch": self.batch, "block": self.width,
+                "vocab": self.vocab}
+
+    def cpu_baseline(self, threads):
+        from oracle import verify as ov
+        torch.set_num_threads(threads)
+        rows = 32
+        x = self.logits[:rows].cpu()
+        p = self.params
+        b = rows // self.width
+        med, n = time_cpu(lambda: ov.target_probs(x, temperatures=p.temperatures[:b].cpu(),
+                                                  top_ks=p.top_ks[:b].cpu(), top_ps=p.top_ps[:b].cpu(),
+                                                  min_ps=p.min_ps[:b].cpu(), rows_per_request=self.width))
+        return {"value": rows * self.vocab * 6 / med / 1e9, "threads": threads,
+                "sample": f"{rows} rows x {self.vocab}, oracle torch-CPU target distribution, median of {n} runs"}
+
+
 class HbmCopy:
     """Plain device copy of 1 GiB (torch copy_), the calibration kernel for the
     FETCH_SIZE / WRITE_SIZE counters: it reads and writes exactly 1 GiB."""
@@ -387,7 +469,8 @@ class HbmCopy:
                 "sample": f"128 MiB host copy, median of {n} runs"}
 
 
-WORKLOADS = {w.name: w for w in (GreedyVerify, StochasticVerify, WindowGather, SummaryUpdate, HbmCopy)}
+WORKLOADS = {w.name: w for w in (GreedyVerify, StochasticVerify, WindowGather, SummaryUpdate, SoftmaxTempWorkload,
+                                  TargetProbsWorkload, HbmCopy)}
 DEFAULT_WORKLOAD = "verify_sample"
 
 

@@ -255,6 +255,50 @@ LS_API int ls_verify_sample(const ls_verify_sample_args* args, void* counters, u
                             void* scratch, uint64_t scratch_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------
+ * Dense target distributions.
+ *
+ * ls_softmax_temp replaces SoftmaxTemp.execute
+ * (SRT/speculative/dspark_components/kernels/softmax_temp.py:17-175):
+ *   out[r, v] = softmax_v(logits[r, v] / temperatures[r / rows_per_request])
+ *   as fp32, rows = batch * rows_per_request, out row stride out_row_stride.
+ *
+ * ls_target_probs replaces build_dflash_verify_target_probs
+ * (SRT/speculative/dflash_utils.py:743-810): each row's distribution after
+ * temperature, top-k (ties at the k-th value to the lowest index) and top-p,
+ * written dense as fp32 [rows, vocab] with zeros outside the support.
+ * top_ks / top_ps / min_ps as in ls_verify_sample (min-p, applied after
+ * top-p, is not part of the reference function: pass NULL to match it).
+ * Workspace from ls_target_probs_workspace.  A row whose support exceeds the
+ * kernel's capacity is written as zeros and sets *status (may be NULL) to 1.
+ * ------------------------------------------------------------------------- */
+LS_API int ls_softmax_temp(const void* logits, int32_t logits_dtype, int64_t logits_row_stride, int64_t rows,
+                           int64_t vocab, const float* temperatures, int32_t rows_per_request, float* out,
+                           int64_t out_row_stride, void* stream);
+
+typedef struct {
+  const void* logits;
+  int32_t logits_dtype;
+  int64_t logits_row_stride;
+  int64_t batch;
+  int32_t rows_per_request;
+  int64_t vocab;
+  const float* temperatures;
+  const int32_t* top_ks;
+  const float* top_ps;
+  const float* min_ps;
+  int32_t max_top_k; /* host upper bound of top_ks (0 = 1024) */
+  float* out;
+  int64_t out_row_stride;
+  int32_t* status;
+  int32_t scan_hint; /* as in ls_verify_sample */
+} ls_target_probs_args;
+
+LS_API int ls_target_probs_workspace(int64_t batch, int32_t rows_per_request, int64_t vocab, int32_t max_top_k,
+                                     uint64_t* counter_bytes, uint64_t* scratch_bytes);
+LS_API int ls_target_probs(const ls_target_probs_args* args, void* counters, uint64_t counter_bytes, void* scratch,
+                           uint64_t scratch_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
  * Split-engine verification on dense target probabilities.
  *
  * ls_decide_acceptance replaces src/longspark/engine/sampling.py:19-35

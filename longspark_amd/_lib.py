@@ -57,6 +57,16 @@ class VerifySampleArgs(ctypes.Structure):
     ]
 
 
+class TargetProbsArgs(ctypes.Structure):
+    """Mirror of ``ls_target_probs_args``."""
+    _fields_ = [
+        ("logits", P), ("logits_dtype", I32), ("logits_row_stride", I64),
+        ("batch", I64), ("rows_per_request", I32), ("vocab", I64),
+        ("temperatures", P), ("top_ks", P), ("top_ps", P), ("min_ps", P), ("max_top_k", I32),
+        ("out", P), ("out_row_stride", I64), ("status", P), ("scan_hint", I32),
+    ]
+
+
 class KvRows(ctypes.Structure):
     """Mirror of ``ls_kv_rows``."""
     _fields_ = [
@@ -93,6 +103,9 @@ _SIGNATURES = {
     "ls_adjust_logits": (I32, [P, I32, I64, I64, I64, I32, P, P, I64, P, I64, P, I32, P, I64, I32, I64, P]),
     "ls_verify_sample_workspace": (I32, [I64, I32, I64, I32, P, P]),
     "ls_verify_sample": (I32, [ctypes.POINTER(VerifySampleArgs), P, U64, P, U64, P]),
+    "ls_softmax_temp": (I32, [P, I32, I64, I64, I64, P, I32, P, I64, P]),
+    "ls_target_probs_workspace": (I32, [I64, I32, I64, I32, P, P]),
+    "ls_target_probs": (I32, [ctypes.POINTER(TargetProbsArgs), P, U64, P, U64, P]),
     "ls_decide_acceptance": (I32, [P, I32, I64, I64, P, I64, P, I64, P, I64, I64, I64, I32, I64, P, P, I64, P]),
     "ls_finish_sampling": (I32, [P, I64, P, I64, P, I64, P, I64, I64, P, P]),
     "ls_finalize_verify_outputs": (I32, [P, I32, I64, I64, P, I32, I64, P, I32, I64, P, I32, I64, I64, I32, P, P, P,

@@ -114,6 +114,22 @@ __device__ __forceinline__ uint4 load16_stream(const void* p) {
   return r;
 }
 
+// 16-byte non-temporal store (the data is consumed by another kernel).
+__device__ __forceinline__ void store16_stream(void* p, const uint4& v) {
+  uint4* q = reinterpret_cast<uint4*>(p);
+  __builtin_nontemporal_store(v.x, &q->x);
+  __builtin_nontemporal_store(v.y, &q->y);
+  __builtin_nontemporal_store(v.z, &q->z);
+  __builtin_nontemporal_store(v.w, &q->w);
+}
+__device__ __forceinline__ void store16_stream(void* p, const float4& v) {
+  float4* q = reinterpret_cast<float4*>(p);
+  __builtin_nontemporal_store(v.x, &q->x);
+  __builtin_nontemporal_store(v.y, &q->y);
+  __builtin_nontemporal_store(v.z, &q->z);
+  __builtin_nontemporal_store(v.w, &q->w);
+}
+
 // ------------------------------------------------------ wave reductions ---
 
 __device__ __forceinline__ float wave_max(float v) {

@@ -1,0 +1,172 @@
+// Dense temperature softmax: out[r, v] = softmax_v(logits[r, v] / T[r / rows_per_request])
+// (SRT/speculative/dspark_components/kernels/softmax_temp.py:69-175; the
+// torch form :69-86 defines the values, x = logit / T then softmax).
+//
+// One workgroup of 1024 threads per row.  The first pass reads the row once
+// and keeps, per thread, an online maximum and the sum of exponentials
+// rescaled whenever the maximum rises; the per-thread pairs are combined
+// across the workgroup.  The second pass reads the row again (it is still
+// in the last-level cache for the rows in flight) and writes the
+// probabilities as fp32.  Rows 16-byte aligned (start and stride) move
+// as 16-byte vectors; others element by element.
+#include "rowscan.h"
+
+namespace ls {
+namespace {
+
+constexpr int kST = 1024;   // threads per row
+constexpr int kSTU = 4;     // vectors per thread in flight
+
+// Values: p = exp2((l - l_max) * c2) / sum, c2 = log2(e) / T, which is the
+// reference's exp(l / T - max(l / T)) / sum up to the rounding of its fp32
+// quotient (a relative difference of about |l - l_max| / T * 2^-24 in p).
+// The per-thread sums are kept in fp64 (one fp32 partial per vector).
+
+template <typename Tag, bool kVec>
+__global__ __launch_bounds__(kST) void softmax_temp_kernel(const typename Tag::storage* __restrict__ logits,
+                                                           int64_t lrs, int64_t vocab,
+                                                           const float* __restrict__ temps, int rpr,
+                                                           float* __restrict__ out, int64_t ors) {
+  using S = typename Tag::storage;
+  constexpr int P = Tag::kPerVec;
+  __shared__ float wm[kST / kWave];
+  __shared__ double wsum[kST / kWave];
+  const int64_t row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1), wid = tid / kWave;
+  const float c2 = 1.4426950408889634f / temps[row / rpr];
+  const S* rp = logits + row * lrs;
+  float* op = out + row * ors;
+  const int64_t nvec = kVec ? vocab / P : 0;
+  const uint4* vp = reinterpret_cast<const uint4*>(rp);
+
+  // pass 1: per-thread maximum of l and sum of exp2((l - max) * c2)
+  float m = -INFINITY;
+  double s = 0.0;
+  auto add = [&](const float* x, int n) __attribute__((always_inline)) {
+    float vm = x[0];
+#pragma unroll
+    for (int q = 1; q < P; ++q)
+      if (q < n) vm = fmaxf(vm, x[q]);
+    if (vm > m) {
+      if (m != -INFINITY) s *= static_cast<double>(__builtin_amdgcn_exp2f((m - vm) * c2));
+      m = vm;
+    }
+    if (m != -INFINITY) {
+      float vs = 0.f;
+#pragma unroll
+      for (int q = 0; q < P; ++q)
+        if (q < n) vs += __builtin_amdgcn_exp2f((x[q] - m) * c2);
+      s += static_cast<double>(vs);
+    }
+  };
+  if constexpr (kVec) {
+    for (int64_t v0 = tid; v0 < nvec; v0 += kSTU * kST) {
+      uint4 buf[kSTU];  // ordinary loads: the row stays cached for the second pass
+#pragma unroll
+      for (int u = 0; u < kSTU; ++u) buf[u] = load16(vp + min<int64_t>(v0 + u * kST, nvec - 1));
+#pragma unroll
+      for (int u = 0; u < kSTU; ++u) {
+        if (v0 + u * kST < nvec) {
+          float x[P];
+          unpack16<Tag>(buf[u], x);
+          add(x, P);
+        }
+      }
+    }
+  }
+  for (int64_t e = nvec * P + tid; e < vocab; e += kST) {
+    float x[P];
+    x[0] = to_f32<S>(rp[e]);
+    add(x, 1);
+  }
+
+  // combine the (max, sum) pairs: within the wave, then across waves
+#pragma unroll
+  for (int o = kWave / 2; o > 0; o >>= 1) {
+    const float m2 = __shfl_xor(m, o, kWave);
+    const double s2 = __shfl_xor(s, o, kWave);
+    const float mm = fmaxf(m, m2);
+    s = (m == -INFINITY ? 0.0 : s * static_cast<double>(__builtin_amdgcn_exp2f((m - mm) * c2))) +
+        (m2 == -INFINITY ? 0.0 : s2 * static_cast<double>(__builtin_amdgcn_exp2f((m2 - mm) * c2)));
+    m = mm;
+  }
+  if (lane == 0) {
+    wm[wid] = m;
+    wsum[wid] = s;
+  }
+  __syncthreads();
+  float rm = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < kST / kWave; ++w) rm = fmaxf(rm, wm[w]);
+  double z = 0.0;
+#pragma unroll
+  for (int w = 0; w < kST / kWave; ++w)
+    if (wm[w] != -INFINITY) z += wsum[w] * static_cast<double>(__builtin_amdgcn_exp2f((wm[w] - rm) * c2));
+  const float inv = static_cast<float>(1.0 / z);
+
+  // pass 2: p = exp2((l - max) * c2) / sum
+  if constexpr (kVec) {
+    for (int64_t v0 = tid; v0 < nvec; v0 += kSTU * kST) {
+      uint4 buf[kSTU];
+#pragma unroll
+      for (int u = 0; u < kSTU; ++u) buf[u] = load16_stream(vp + min<int64_t>(v0 + u * kST, nvec - 1));
+#pragma unroll
+      for (int u = 0; u < kSTU; ++u) {
+        const int64_t v = v0 + u * kST;
+        if (v < nvec) {
+          float x[P];
+          unpack16<Tag>(buf[u], x);
+          float4* o4 = reinterpret_cast<float4*>(op + v * P);
+#pragma unroll
+          for (int h = 0; h < P / 4; ++h) {
+            float4 y;
+            y.x = __builtin_amdgcn_exp2f((x[4 * h + 0] - rm) * c2) * inv;
+            y.y = __builtin_amdgcn_exp2f((x[4 * h + 1] - rm) * c2) * inv;
+            y.z = __builtin_amdgcn_exp2f((x[4 * h + 2] - rm) * c2) * inv;
+            y.w = __builtin_amdgcn_exp2f((x[4 * h + 3] - rm) * c2) * inv;
+            store16_stream(o4 + h, y);
+          }
+        }
+      }
+    }
+  }
+  for (int64_t e = nvec * P + tid; e < vocab; e += kST)
+    op[e] = __builtin_amdgcn_exp2f((to_f32<S>(rp[e]) - rm) * c2) * inv;
+}
+
+}  // namespace
+}  // namespace ls
+
+extern "C" int ls_softmax_temp(const void* logits, int32_t logits_dtype, int64_t logits_row_stride, int64_t rows,
+                               int64_t vocab, const float* temperatures, int32_t rows_per_request, float* out,
+                               int64_t out_row_stride, void* stream) {
+  using namespace ls;
+  LS_CHECK(logits && temperatures && out, LS_ERR_VALUE, "ls_softmax_temp: null pointer");
+  LS_CHECK(rows > 0 && vocab > 0 && rows_per_request > 0 && rows % rows_per_request == 0, LS_ERR_SHAPE,
+           "ls_softmax_temp: rows must be a positive multiple of rows_per_request");
+  LS_CHECK(rows < (int64_t(1) << 31), LS_ERR_SHAPE, "ls_softmax_temp: too many rows");
+  LS_CHECK(logits_row_stride >= vocab && out_row_stride >= vocab, LS_ERR_SHAPE, "ls_softmax_temp: row stride < vocab");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const dim3 grid(static_cast<unsigned>(rows));
+  const bool out_vec = aligned16(out) && (out_row_stride * 4) % 16 == 0;
+#define LS_ST(TAG)                                                                                              \
+  do {                                                                                                          \
+    using S = typename TAG::storage;                                                                            \
+    const S* lp = static_cast<const S*>(logits);                                                                \
+    const bool vec = out_vec && aligned16(logits) && (logits_row_stride * int64_t(sizeof(S))) % 16 == 0;       \
+    if (vec)                                                                                                    \
+      softmax_temp_kernel<TAG, true><<<grid, kST, 0, st>>>(lp, logits_row_stride, vocab, temperatures,         \
+                                                          rows_per_request, out, out_row_stride);              \
+    else                                                                                                        \
+      softmax_temp_kernel<TAG, false><<<grid, kST, 0, st>>>(lp, logits_row_stride, vocab, temperatures,        \
+                                                           rows_per_request, out, out_row_stride);             \
+  } while (0)
+  if (logits_dtype == LS_BF16) LS_ST(BF16);
+  else if (logits_dtype == LS_F32) LS_ST(F32);
+  else if (logits_dtype == LS_F16) LS_ST(F16);
+  else return fail(LS_ERR_DTYPE, "ls_softmax_temp: logits must be bf16, fp16 or fp32");
+#undef LS_ST
+  LS_LAUNCH_CHECK();
+  return LS_OK;
+}

@@ -33,14 +33,6 @@ __device__ __forceinline__ int64_t ld_any(const void* p, int dtype, int64_t i) {
   return dtype == LS_I64 ? ld_index<int64_t>(p, i) : ld_index<int32_t>(p, i);
 }
 
-__device__ __forceinline__ void store16_stream(void* p, const uint4& v) {
-  uint4* q = reinterpret_cast<uint4*>(p);
-  __builtin_nontemporal_store(v.x, &q->x);
-  __builtin_nontemporal_store(v.y, &q->y);
-  __builtin_nontemporal_store(v.z, &q->z);
-  __builtin_nontemporal_store(v.w, &q->w);
-}
-
 __global__ __launch_bounds__(kGT) void raw_page_table_kernel(const int32_t* __restrict__ rtt, int64_t rtt_sb,
                                                              int64_t rtt_st, const void* slots, int slots_dtype,
                                                              const void* seq_lens, int seq_dtype, int window,

@@ -141,6 +141,7 @@ struct Shared {
   uint64_t buf[kNBuf];
   uint32_t hist[256];
   float red_f[kT / kWave * 2];
+  double red_d[kT / kWave];
   int red_i[kT / kWave];
   int count;
   int sel_digit;
@@ -292,6 +293,20 @@ __device__ __forceinline__ float block_sum(Shared& sh, float v) {
   __syncthreads();
   float t = 0.f;
   for (int w = 0; w < kT / kWave; ++w) t += sh.red_f[w];
+  __syncthreads();
+  return t;
+}
+
+// fp64 block sum (masses that decide a top-p / min-p boundary).
+__device__ __forceinline__ double block_sum_d(Shared& sh, double v) {
+#pragma unroll
+  for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave;
+  __syncthreads();
+  if (lane == 0) sh.red_d[wid] = v;
+  __syncthreads();
+  double t = 0.0;
+  for (int w = 0; w < kT / kWave; ++w) t += sh.red_d[w];
   __syncthreads();
   return t;
 }

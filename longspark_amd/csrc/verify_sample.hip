@@ -125,7 +125,8 @@ __device__ __forceinline__ void atomic_put_u64(uint64_t* p, uint64_t v) {
 struct ScanOut {
   float mx;   // running max of x (thread)
   float mz;   // reference max of z (thread)
-  float z;    // sum exp((x - mz) / T) (thread)
+  double z;   // sum exp((x - mz) / T) (thread), accumulated in fp64: it
+              // decides top-p / min-p boundaries over the whole row
 };
 
 constexpr int kMaint = 4;  // steps between maintenance points
@@ -354,11 +355,13 @@ __device__ ScanOut scan_range(Shared& sh, const typename Tag::storage* row, int6
     for (int q = 1; q < P; ++q) vmax = fmaxf(vmax, x[q]);
     if (need_z) {
       if (vmax > o.mz) {
-        o.z *= __builtin_amdgcn_exp2f((o.mz - vmax) * c2);
+        o.z *= static_cast<double>(__builtin_amdgcn_exp2f((o.mz - vmax) * c2));
         o.mz = vmax;
       }
+      float vs = 0.f;
 #pragma unroll
-      for (int q = 0; q < P; ++q) o.z += __builtin_amdgcn_exp2f((x[q] - o.mz) * c2);
+      for (int q = 0; q < P; ++q) vs += __builtin_amdgcn_exp2f((x[q] - o.mz) * c2);
+      o.z += static_cast<double>(vs);
     }
     o.mx = fmaxf(o.mx, vmax);
     const float tau_eff = fmaxf(tau, o.mx + off_x);
@@ -597,8 +600,10 @@ __device__ __forceinline__ ScanOut finish_slice(Shared& sh, const ScanOut& o, in
   r.mx = block_max(sh, o.mx);
   if (mode != kModeTopK) {
     const float gm = r.mx;
-    float zt = (o.mz == -FLT_MAX) ? 0.f : o.z * __builtin_amdgcn_exp2f((o.mz - gm) * (1.4426950408889634f / t));
-    r.z = block_sum(sh, zt);
+    const double zt = (o.mz == -FLT_MAX)
+                          ? 0.0
+                          : o.z * static_cast<double>(__builtin_amdgcn_exp2f((o.mz - gm) * (1.4426950408889634f / t)));
+    r.z = block_sum_d(sh, zt);
     r.mz = gm;
   } else {
     r.z = 0.f;
@@ -621,31 +626,34 @@ __device__ __forceinline__ ScanOut finish_slice(Shared& sh, const ScanOut& o, in
 
 // Index of the first entry i < n (entries sorted by key, e_i = exp(s_i - m))
 // at which the running sum before i, divided by `denom`, exceeds `limit`;
-// n if none.  Also returns the full sum of e_i / denom through *total.
-__device__ __forceinline__ int first_excl_exceeds(Shared& sh, int n, float m, float denom, float limit, float* total) {
+// n if none.  Also returns the full sum of e_i / denom through *total.  The
+// running sum is kept in fp64 (it decides the top-p boundary).
+__device__ __forceinline__ int first_excl_exceeds(Shared& sh, int n, float m, double denom, float limit,
+                                                  float* total) {
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1), wid = tid / kWave;
   __shared__ int found;
-  __shared__ float wsum[kT / kWave];
+  __shared__ double wsum[kT / kWave];
   if (tid == 0) found = n;
-  float carry = 0.f;
+  const double lim = static_cast<double>(limit) * denom;
+  double carry = 0.0;
   __syncthreads();
   for (int r = 0; r < n; r += kT) {
     const int i = r + tid;
-    const float p = i < n ? __expf(key_s(sh.buf[i]) - m) / denom : 0.f;
-    float inc = p;
+    const double e = i < n ? static_cast<double>(__expf(key_s(sh.buf[i]) - m)) : 0.0;
+    double inc = e;
 #pragma unroll
     for (int o = 1; o < kWave; o <<= 1) {
-      float v = __shfl_up(inc, o, kWave);
+      const double v = __shfl_up(inc, o, kWave);
       if (lane >= o) inc += v;
     }
     if (lane == kWave - 1) wsum[wid] = inc;
     __syncthreads();
-    float before = carry;
+    double before = carry;
     for (int w = 0; w < wid; ++w) before += wsum[w];
-    const float excl = before + inc - p;
-    if (i < n && excl > limit) atomicMin(&found, i);
-    float tot = 0.f;
+    const double excl = before + inc - e;
+    if (i < n && excl > lim) atomicMin(&found, i);
+    double tot = 0.0;
     for (int w = 0; w < kT / kWave; ++w) tot += wsum[w];
     carry += tot;
     __syncthreads();
@@ -653,7 +661,7 @@ __device__ __forceinline__ int first_excl_exceeds(Shared& sh, int n, float m, fl
     __syncthreads();  // all threads have read `found` before any thread updates it again
     if (f < n) break;
   }
-  if (total) *total = carry;
+  if (total) *total = static_cast<float>(carry / denom);
   const int res = found;
   __syncthreads();
   return res;
@@ -670,7 +678,7 @@ __device__ __forceinline__ int first_excl_exceeds(Shared& sh, int n, float m, fl
 
 struct Hist {
   uint32_t cnt[256];
-  float mass[256];
+  double mass[256];  // fp64: the masses decide top-p boundaries
 };
 
 // One pass over the row: histogram of digit (key >> shift) & 255 of every key
@@ -680,7 +688,7 @@ __device__ __noinline__ void hist_pass(Hist& h, const typename Tag::storage* row
                                        float t, float m, uint64_t kmin, uint64_t prefix, uint64_t pmask, int shift) {
   const int tid = threadIdx.x;
   h.cnt[tid] = 0;
-  h.mass[tid] = 0.f;
+  h.mass[tid] = 0.0;
   __syncthreads();
   for (int64_t v = tid; v < vocab; v += kT) {
     const float s = transform1(f, to_f32<typename Tag::storage>(row[v]), v) / t;
@@ -688,7 +696,7 @@ __device__ __noinline__ void hist_pass(Hist& h, const typename Tag::storage* row
     if (key >= kmin && (key & pmask) == prefix) {
       const int d = static_cast<int>((key >> shift) & 255u);
       atomicAdd(&h.cnt[d], 1u);
-      atomicAdd(&h.mass[d], __expf(s - m));
+      atomicAdd(&h.mass[d], static_cast<double>(__expf(s - m)));
     }
   }
   __syncthreads();
@@ -725,15 +733,15 @@ __device__ __noinline__ uint64_t select_key_by_count(Hist& h, const typename Tag
 // > K and >= kmin) is <= limit: the last entry a top-p cut keeps.
 template <typename Tag>
 __device__ __noinline__ uint64_t select_key_by_mass(Hist& h, const typename Tag::storage* row, int64_t vocab,
-                                                    const XForm& f, float t, float m, uint64_t kmin, float limit) {
+                                                    const XForm& f, float t, float m, uint64_t kmin, double limit) {
   __shared__ int s_d;
-  __shared__ float s_above;
+  __shared__ double s_above;
   uint64_t prefix = 0, pmask = 0;
-  float above = 0.f;
+  double above = 0.0;
   for (int shift = 56; shift >= 0; shift -= 8) {
     hist_pass<Tag>(h, row, vocab, f, t, m, kmin, prefix, pmask, shift);
     if (threadIdx.x == 0) {
-      float cum = above, sel_above = above;
+      double cum = above, sel_above = above;
       int sel = -1;
       for (int d = 255; d >= 0; --d) {
         if (h.cnt[d] == 0) continue;
@@ -761,26 +769,26 @@ __device__ __noinline__ uint64_t select_key_by_mass(Hist& h, const typename Tag:
 // kmin with exp(s - m) >= emin (as an ordered value, 0xffffffff if none).
 template <typename Tag>
 __device__ __noinline__ void tally(Shared& sh, const typename Tag::storage* row, int64_t vocab, const XForm& f, float t,
-                                   float m, uint64_t kmin, float emin, int* count, float* mass, uint32_t* smin_ord) {
+                                   float m, uint64_t kmin, float emin, int* count, double* mass, uint32_t* smin_ord) {
   __shared__ unsigned s_cnt, s_min;
   const int tid = threadIdx.x;
   if (tid == 0) { s_cnt = 0; s_min = 0xffffffffu; }
   __syncthreads();
-  float acc = 0.f;
+  double acc = 0.0;
   unsigned c = 0, mn = 0xffffffffu;
   for (int64_t v = tid; v < vocab; v += kT) {
     const float s = transform1(f, to_f32<typename Tag::storage>(row[v]), v) / t;
     const uint64_t key = cand_key(s, static_cast<int>(v));
     if (key >= kmin) {
       const float e = __expf(s - m);
-      acc += e;
+      acc += static_cast<double>(e);
       ++c;
       if (e >= emin) mn = min(mn, static_cast<unsigned>(key >> 32));
     }
   }
   atomicAdd(&s_cnt, c);
   atomicMin(&s_min, mn);
-  const float tot = block_sum(sh, acc);
+  const double tot = block_sum_d(sh, acc);
   *count = static_cast<int>(s_cnt);
   *mass = tot;
   *smin_ord = s_min;
@@ -811,16 +819,16 @@ __device__ __noinline__ int collect(Shared& sh, const typename Tag::storage* row
 // of a row that was never scanned (two passes; fallback only).
 template <typename Tag>
 __device__ __noinline__ void row_stats(Shared& sh, const typename Tag::storage* row, int64_t vocab, const XForm& f,
-                                       float t, float* m_x, float* z) {
+                                       float t, float* m_x, double* z) {
   float mx = -FLT_MAX;
   for (int64_t v = threadIdx.x; v < vocab; v += kT)
     mx = fmaxf(mx, transform1(f, to_f32<typename Tag::storage>(row[v]), v));
   mx = block_max(sh, mx);
-  float acc = 0.f;
+  double acc = 0.0;
   for (int64_t v = threadIdx.x; v < vocab; v += kT)
-    acc += __expf((transform1(f, to_f32<typename Tag::storage>(row[v]), v) - mx) / t);
+    acc += static_cast<double>(__expf((transform1(f, to_f32<typename Tag::storage>(row[v]), v) - mx) / t));
   *m_x = mx;
-  *z = block_sum(sh, acc);
+  *z = block_sum_d(sh, acc);
 }
 
 struct Exact {
@@ -833,15 +841,15 @@ struct Exact {
 // sum over the row of exp(s - m) (filter / dense modes).
 template <typename Tag>
 __device__ __noinline__ Exact exact_support(Shared& sh, const typename Tag::storage* row, int64_t vocab,
-                                            const XForm& f, const Params& p, int mode, float m_x, float z_dense) {
+                                            const XForm& f, const Params& p, int mode, float m_x, double z_dense) {
   __shared__ Hist h;
   const float t = p.temperature;
   Exact r;
   r.m = m_x / t;
   uint64_t kmin = 0;
-  float z1 = z_dense;
+  double z1 = z_dense;
   int cnt;
-  float mass;
+  double mass;
   uint32_t smin;
   if (mode == kModeTopK && p.top_k < vocab) {
     kmin = select_key_by_count<Tag>(h, row, vocab, f, t, r.m, p.top_k);
@@ -852,10 +860,11 @@ __device__ __noinline__ Exact exact_support(Shared& sh, const typename Tag::stor
   if (p.min_p > 0.f) {
     // Over the top-p set: p2 = (e / z1) / P with P its mass; drop p2 < p2_max * min_p.
     tally<Tag>(sh, row, vocab, f, t, r.m, kcut, INFINITY, &cnt, &mass, &smin);
-    const float pp = mass / z1;
-    const float thr = ((1.0f / z1) / pp) * p.min_p;
+    const float pp = static_cast<float>(mass / z1);
+    const float z1f = static_cast<float>(z1);
+    const float thr = ((1.0f / z1f) / pp) * p.min_p;
     // keep e with (e / z1) / pp >= thr: find the smallest such s
-    float emin = thr * pp * z1;
+    float emin = thr * pp * z1f;
     tally<Tag>(sh, row, vocab, f, t, r.m, kcut, emin, &cnt, &mass, &smin);
     if (smin != 0xffffffffu) {
       const uint64_t kmp = static_cast<uint64_t>(smin) << 32;
@@ -863,7 +872,7 @@ __device__ __noinline__ Exact exact_support(Shared& sh, const typename Tag::stor
     }
   }
   tally<Tag>(sh, row, vocab, f, t, r.m, kcut, INFINITY, &cnt, &mass, &smin);
-  r.z = mass;
+  r.z = static_cast<float>(mass);
   r.kcut = kcut;
   r.n = cnt;
   return r;
@@ -891,7 +900,7 @@ __device__ __forceinline__ void finalize_row(Shared& sh, const ScanOut& st, cons
   if (mode == kModeDense) {
     if (tid == 0) {
       s_m = st.mx / t;
-      s_z = st.z;
+      s_z = static_cast<float>(st.z);
       s_n = -1;
       s_flags |= kFlagDense;
     }
@@ -902,18 +911,19 @@ __device__ __forceinline__ void finalize_row(Shared& sh, const ScanOut& st, cons
       sort_desc(sh, n);
       if (mode == kModeTopK && n > p.top_k) n = p.top_k;
       const float m = n > 0 ? key_s(sh.buf[0]) : -INFINITY;
-      float z1;
+      double z1d;
       if (mode == kModeTopK) {
         float acc = 0.f;
         for (int i = tid; i < n; i += kT) acc += __expf(key_s(sh.buf[i]) - m);
-        z1 = block_sum(sh, acc);
+        z1d = block_sum_d(sh, static_cast<double>(acc));
       } else {
-        z1 = st.z;  // dense normaliser relative to the row maximum
+        z1d = st.z;  // dense normaliser relative to the row maximum
       }
+      const float z1 = static_cast<float>(z1d);
       int n_f = n;
       float mass_all = 0.f;
       if (p.top_p < 1.0f && n > 0) {
-        n_f = first_excl_exceeds(sh, n, m, z1, p.top_p, &mass_all);
+        n_f = first_excl_exceeds(sh, n, m, z1d, p.top_p, &mass_all);
         if (mode == kModeFilter && p.min_p <= 0.f && n_f == n && mass_all <= p.top_p) {
           if (tid == 0) { s_flags |= kFlagOverflow; s_why |= kWhyNucleus; }  // nucleus open
         }
@@ -955,7 +965,7 @@ __device__ __forceinline__ void finalize_row(Shared& sh, const ScanOut& st, cons
     if (tid == 0) {
       RowRec r{};
       r.m = st.mx;  // x-domain maximum
-      r.z = st.z;   // dense normaliser (filter / dense modes)
+      r.z = static_cast<float>(st.z);   // dense normaliser (filter / dense modes)
       r.flags = kFlagOverflow;
       r.why = s_why;
       *rec = r;
@@ -1010,7 +1020,7 @@ __device__ __forceinline__ bool merge_slices(Shared& sh, ScanOut& st, int mode, 
   if (tid == 0) {
     atomic_put_u64(pubs + 2 * slice, ovf ? ~uint64_t(0) : static_cast<uint64_t>(n));
     atomic_put_u64(pubs + 2 * slice + 1,
-                   (static_cast<uint64_t>(ordered_f32(st.mx)) << 32) | __float_as_uint(st.z));
+                   (static_cast<uint64_t>(ordered_f32(st.mx)) << 32) | __float_as_uint(static_cast<float>(st.z)));
   }
   __syncthreads();  // every thread's publishes have completed
   if (tid == 0) is_last = (arrive(counter) == static_cast<uint32_t>(slices - 1));
@@ -1018,6 +1028,7 @@ __device__ __forceinline__ bool merge_slices(Shared& sh, ScanOut& st, int mode, 
   if (!is_last) return false;
   __shared__ int offs[17];
   __shared__ float smx[16], sz[16];
+  __shared__ double s_zm;
   if (tid == 0) {
     atomic_take_u32(counter);
     int total = 0, bad = 0;
@@ -1033,20 +1044,22 @@ __device__ __forceinline__ bool merge_slices(Shared& sh, ScanOut& st, int mode, 
     offs[slices] = total;
     sh.overflow = (bad || total > kNBuf) ? kWhyMerge : 0;
     sh.count = sh.overflow ? 0 : total;
-    float gm = -FLT_MAX, z = 0.f;
+    float gm = -FLT_MAX;
+    double z = 0.0;
     for (int s = 0; s < slices; ++s) gm = fmaxf(gm, smx[s]);
     if (mode != kModeTopK) {
       const float c2 = 1.4426950408889634f / t;
       for (int s = 0; s < slices; ++s)
-        if (smx[s] != -FLT_MAX) z += sz[s] * __builtin_amdgcn_exp2f((smx[s] - gm) * c2);
+        if (smx[s] != -FLT_MAX)
+          z += static_cast<double>(sz[s]) * static_cast<double>(__builtin_amdgcn_exp2f((smx[s] - gm) * c2));
     }
     smx[0] = gm;
-    sz[0] = z;
+    s_zm = z;
   }
   __syncthreads();
   st.mx = smx[0];
   st.mz = smx[0];
-  st.z = sz[0];
+  st.z = s_zm;
   if (!sh.overflow) {
     for (int s = 0; s < slices; ++s) {
       const int base = offs[s], cnt = offs[s + 1] - offs[s];
@@ -1157,7 +1170,7 @@ __global__ __launch_bounds__(kT) void cand_prep_kernel(Args a) {
   const int64_t b = row / a.width;
   const int j = static_cast<int>(row % a.width);
   CandRec cr{NAN, -1};
-  if (j < a.width - 1) {
+  if (a.cand && j < a.width - 1) {
     const int64_t c = cand_at<CandT>(a, b, j);
     if (c >= 0 && c < a.vocab) {
       using S = typename TagT::storage;
@@ -2081,7 +2094,7 @@ __device__ __forceinline__ RowRec draft_merge_block(const Args& a, WaveShared& w
 
 // Draft slices of a launch that runs after the target fallback.
 template <typename TagD, typename CandT>
-__global__ __launch_bounds__(kWave) void draft_wave_kernel(Args a) {
+__global__ __launch_bounds__(kWave, 2) void draft_wave_kernel(Args a) {
   __shared__ WaveShared ws;
   draft_wave_slice<TagD, CandT, false>(a, ws, blockIdx.x / a.dslices, blockIdx.x % a.dslices);
 }
@@ -2095,7 +2108,7 @@ __global__ __launch_bounds__(kWave) void draft_wave_kernel(Args a) {
 // are dispatched in order on each XCD, so every target row is resident or
 // done before a draft slice of the same XCD waits).
 template <typename TagT, typename TagD, typename CandT>
-__global__ __launch_bounds__(kWave) void verify_wave_kernel(Args a) {
+__global__ __launch_bounds__(kWave, 2) void verify_wave_kernel(Args a) {
   __shared__ WaveShared ws;
   using S = typename TagT::storage;
   constexpr int P = TagT::kPerVec;
@@ -2197,7 +2210,8 @@ __global__ __launch_bounds__(kT) void target_fallback_kernel(Args a) {
     const XForm f = target_xform(a, b, row);
     const CandRec cr = a.cand_rec[row];
     const int mode = row_mode(p, a.vocab);
-    float m_x = prev.m, z = prev.z;
+    float m_x = prev.m;
+    double z = prev.z;
     if (prev.flags & kFlagUnscanned) row_stats<TagT>(sh, rp, a.vocab, f, p.temperature, &m_x, &z);
     const Exact ex = exact_support<TagT>(sh, rp, a.vocab, f, p, mode, m_x, z);
     const int n_f = ex.n <= kCap ? collect<TagT>(sh, rp, a.vocab, f, p.temperature, ex.kcut) : 0;
@@ -2216,7 +2230,8 @@ __device__ __forceinline__ void draft_exact_pass(Shared& sh, const Args& a, int6
   const S* rp = static_cast<const S*>(a.draft) + b * a.dsb + static_cast<int64_t>(len) * a.dsk;
   XForm f{nullptr, nullptr, nullptr, 1.f, 0, nullptr};
   const int mode = row_mode(p, a.vocab);
-  float m_x = prev.m, z = prev.z;
+  float m_x = prev.m;
+  double z = prev.z;
   if (prev.flags & kFlagUnscanned) row_stats<TagD>(sh, rp, a.vocab, f, p.temperature, &m_x, &z);
   const Exact ex = exact_support<TagD>(sh, rp, a.vocab, f, p, mode, m_x, z);
   const int n_f = ex.n <= kCap ? collect<TagD>(sh, rp, a.vocab, f, p.temperature, ex.kcut) : 0;
@@ -2232,6 +2247,44 @@ __device__ __forceinline__ float target_p_dense(const Args& a, const RowRec& r, 
   const float s = transform1(f, to_f32<S>(static_cast<const S*>(a.logits)[row * a.lrs + v]), v) / t;
   if (r.last != 0 && cand_key(s, static_cast<int>(v)) < r.last) return 0.f;
   return __expf(s - r.m) / r.z;
+}
+
+// Dense fp32 distribution of target row blockIdx.x from its record (one
+// workgroup per row): zeros, then the support entries; a dense support (no
+// top-k) is evaluated element by element from the logits.  A row the
+// fallback could not resolve (capacity) is left zero and flags *status.
+template <typename TagT>
+__global__ __launch_bounds__(kT) void densify_kernel(Args a, float* out, int64_t ors) {
+  const int64_t row = blockIdx.x;
+  const int64_t b = row / a.width;
+  const int tid = threadIdx.x;
+  if (row == 0 && tid == 0) {  // the fallback worklists return to zero (the call's last kernel)
+    atomic_take_u32(a.list_cnt);
+    atomic_take_u32(a.list_cnt + 1);
+  }
+  const RowRec r = a.rec_t[row];
+  float* op = out + row * ors;
+  if (r.n < 0 && !(r.flags & kFlagOverflow)) {
+    const XForm f = target_xform(a, b, row);
+    const float t = a.temps[b];
+    for (int64_t v = tid; v < a.vocab; v += kT) op[v] = target_p_dense<TagT>(a, r, b, row, v, f, t);
+    return;
+  }
+  int64_t done = 0;
+  if ((reinterpret_cast<uintptr_t>(op) & 15u) == 0) {
+    const int64_t nv = a.vocab / 4;
+    float4* o4 = reinterpret_cast<float4*>(op);
+    const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int64_t v = tid; v < nv; v += kT) store16_stream(o4 + v, z);
+    done = nv * 4;
+  }
+  for (int64_t v = done + tid; v < a.vocab; v += kT) op[v] = 0.f;
+  if (r.flags & kFlagOverflow) {
+    if (tid == 0 && a.status) atomicOr(a.status, kFlagOverflow);
+    return;
+  }
+  __syncthreads();  // the zeros are written before the support entries
+  for (int i = tid; i < r.n; i += kT) op[a.sidx_t[row * kCap + i]] = a.sp_t[row * kCap + i];
 }
 
 template <typename TagD>
@@ -2847,4 +2900,100 @@ extern "C" int ls_verify_sample(const ls_verify_sample_args* in, void* counters,
 #undef LS_RUN
 #undef LS_EVENT
   return fail(LS_ERR_DTYPE, "ls_verify_sample: logits must be bf16, fp16 or fp32");
+}
+
+extern "C" int ls_target_probs_workspace(int64_t batch, int32_t rows_per_request, int64_t vocab, int32_t max_top_k,
+                                         uint64_t* counter_bytes, uint64_t* scratch_bytes) {
+  LS_CHECK(batch > 0 && rows_per_request > 0 && vocab > 0 && counter_bytes && scratch_bytes, LS_ERR_SHAPE,
+           "ls_target_probs_workspace: bad sizes");
+  const int mk = (max_top_k <= 0 || max_top_k > ls::rs::kCap) ? ls::rs::kCap : max_top_k;
+  const ls::Layout l = ls::layout(batch, rows_per_request, vocab, mk);
+  *counter_bytes = l.counters;
+  *scratch_bytes = l.scratch;
+  return LS_OK;
+}
+
+extern "C" int ls_target_probs(const ls_target_probs_args* in, void* counters, uint64_t counter_bytes, void* scratch,
+                               uint64_t scratch_bytes, void* stream) {
+  using namespace ls;
+  LS_CHECK(in, LS_ERR_VALUE, "ls_target_probs: null args");
+  const ls_target_probs_args& x = *in;
+  LS_CHECK(x.batch > 0 && x.rows_per_request > 0 && x.vocab > 0 && x.vocab < (int64_t(1) << 31), LS_ERR_SHAPE,
+           "ls_target_probs: need batch > 0, rows_per_request > 0, 0 < vocab < 2^31");
+  LS_CHECK(x.batch * x.rows_per_request < (int64_t(1) << 31), LS_ERR_SHAPE, "ls_target_probs: too many rows");
+  LS_CHECK(x.logits_row_stride >= x.vocab && x.out_row_stride >= x.vocab, LS_ERR_SHAPE,
+           "ls_target_probs: row stride < vocab");
+  LS_CHECK(x.logits && x.temperatures && x.out, LS_ERR_VALUE, "ls_target_probs: null required pointer");
+  LS_CHECK(x.scan_hint >= 0 && x.scan_hint <= 2, LS_ERR_VALUE, "ls_target_probs: scan_hint must be 0, 1 or 2");
+  const int mk = (x.max_top_k <= 0 || x.max_top_k > rs::kCap) ? rs::kCap : x.max_top_k;
+  const Layout l = layout(x.batch, x.rows_per_request, x.vocab, mk);
+  LS_CHECK(counters && counter_bytes >= l.counters && scratch && scratch_bytes >= l.scratch, LS_ERR_WORKSPACE,
+           "ls_target_probs: needs %llu counter and %llu scratch bytes", (unsigned long long)l.counters,
+           (unsigned long long)l.scratch);
+
+  Args a{};
+  a.logits = x.logits; a.lrs = x.logits_row_stride;
+  a.batch = x.batch; a.width = x.rows_per_request; a.vocab = x.vocab;
+  a.temps = x.temperatures; a.top_ks = x.top_ks; a.top_ps = x.top_ps; a.min_ps = x.min_ps;
+  a.status = x.status;
+  char* c = static_cast<char*>(counters);
+  const int64_t rows = x.batch * x.rows_per_request;
+  a.cnt_t = reinterpret_cast<uint32_t*>(c);
+  a.cnt_d = reinterpret_cast<uint32_t*>(c + up256(4 * rows));
+  a.list_cnt = reinterpret_cast<uint32_t*>(c + up256(4 * rows) + up256(4 * x.batch));
+  a.acc_t = reinterpret_cast<uint64_t*>(c + up256(4 * rows) + up256(4 * x.batch) + 256);
+  char* s = static_cast<char*>(scratch);
+  a.rec_t = reinterpret_cast<RowRec*>(s + l.off_rec_t);
+  a.sidx_t = reinterpret_cast<int32_t*>(s + l.off_sidx_t);
+  a.sp_t = reinterpret_cast<float*>(s + l.off_sp_t);
+  a.rec_d = reinterpret_cast<RowRec*>(s + l.off_rec_d);
+  a.sidx_d = reinterpret_cast<int32_t*>(s + l.off_sidx_d);
+  a.sp_d = reinterpret_cast<float*>(s + l.off_sp_d);
+  a.pub_t = reinterpret_cast<uint64_t*>(s + l.off_pub_t);
+  a.pubs_t = reinterpret_cast<uint64_t*>(s + l.off_pubs_t);
+  a.pub_d = reinterpret_cast<uint64_t*>(s + l.off_pub_d);
+  a.pubs_d = reinterpret_cast<uint64_t*>(s + l.off_pubs_d);
+  a.list_t = reinterpret_cast<int32_t*>(s + l.off_list_t);
+  a.list_d = reinterpret_cast<int32_t*>(s + l.off_list_d);
+  a.cand_rec = reinterpret_cast<CandRec*>(s + l.off_cand);
+  a.s_t = l.s_t;
+  a.s_d = l.s_d;
+  a.hint = x.scan_hint;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const dim3 g_t(static_cast<unsigned>(rows * l.s_t)), g_f(static_cast<unsigned>(rows < 256 ? rows : 256)),
+      g_c(static_cast<unsigned>((rows + rs::kT - 1) / rs::kT)), g_r(static_cast<unsigned>(rows));
+  const bool tvec_ok = aligned16(x.logits);
+#define LS_TP(TT)                                                                                             \
+  do {                                                                                                        \
+    using TS = typename TT::storage;                                                                          \
+    const bool tv = tvec_ok && (x.logits_row_stride * sizeof(TS)) % 16 == 0;                                  \
+    cand_prep_kernel<TT, int32_t><<<g_c, rs::kT, 0, st>>>(a);                                                 \
+    LS_LAUNCH_CHECK();                                                                                        \
+    a.wave = (a.hint != kHintExactOnly && tv && x.vocab / TT::kPerVec >= int64_t(kWave) * kWaveDepth) ? 1 : 0; \
+    a.wave_only = (a.wave && x.max_top_k > 0 && x.max_top_k <= kWaveMaxRowK) ? 1 : 0;                          \
+    if (a.wave) {                                                                                             \
+      verify_wave_kernel<TT, F32, int32_t><<<dim3(static_cast<unsigned>(rows)), kWave, 0, st>>>(a);          \
+      LS_LAUNCH_CHECK();                                                                                      \
+    }                                                                                                         \
+    if (a.hint != kHintExactOnly && !a.wave_only) {                                                           \
+      if (tv) target_scan_kernel<TT, true, int32_t, kPathRaw><<<g_t, rs::kT, 0, st>>>(a);                    \
+      else target_scan_kernel<TT, false, int32_t, kPathRaw><<<g_t, rs::kT, 0, st>>>(a);                      \
+      LS_LAUNCH_CHECK();                                                                                      \
+    }                                                                                                         \
+    if (a.hint != kHintRawOnly) {                                                                             \
+      if (tv) target_scan_kernel<TT, true, int32_t, kPathExact><<<g_t, rs::kT, 0, st>>>(a);                  \
+      else target_scan_kernel<TT, false, int32_t, kPathExact><<<g_t, rs::kT, 0, st>>>(a);                    \
+      LS_LAUNCH_CHECK();                                                                                      \
+    }                                                                                                         \
+    target_fallback_kernel<TT, int32_t><<<g_f, rs::kT, 0, st>>>(a);                                           \
+    LS_LAUNCH_CHECK();                                                                                        \
+    densify_kernel<TT><<<g_r, rs::kT, 0, st>>>(a, x.out, x.out_row_stride);                                   \
+    LS_LAUNCH_CHECK();                                                                                        \
+    return LS_OK;                                                                                             \
+  } while (0)
+  if (x.logits_dtype == LS_BF16) LS_TP(BF16);
+  if (x.logits_dtype == LS_F32) LS_TP(F32);
+  if (x.logits_dtype == LS_F16) LS_TP(F16);
+#undef LS_TP
+  return fail(LS_ERR_DTYPE, "ls_target_probs: logits must be bf16, fp16 or fp32");
 }

@@ -19,11 +19,16 @@ from typing import Dict, Iterable, List, Optional, Tuple
 
 def replacements() -> Dict[str, Dict[str, object]]:
     """module name -> {attribute: replacement}, for every hot-path call site."""
-    from . import kvwindow, penalties, summary, verify
+    from . import dense, kvwindow, penalties, summary, verify
 
     return {
         # greedy verify (SPEC/dspark_components/kernels/accept_greedy.py:22-60)
         "sglang.srt.speculative.dspark_components.kernels.accept_greedy": {"AcceptGreedy": verify.AcceptGreedy},
+        # dense target distributions (SPEC/dspark_components/kernels/softmax_temp.py:17-175,
+        # SPEC/dflash_utils.py:743-810)
+        "sglang.srt.speculative.dspark_components.kernels.softmax_temp": {"SoftmaxTemp": dense.SoftmaxTemp},
+        "sglang.srt.speculative.dflash_utils": {
+            "build_dflash_verify_target_probs": dense.build_dflash_verify_target_probs},
         # split-engine two-phase rejection sampling (src/longspark/engine/sampling.py:19-57)
         "longspark.engine.sampling": {"decide_acceptance": verify.decide_acceptance,
                                       "finish_sampling": verify.finish_sampling},

@@ -298,7 +298,7 @@ def min_p_renorm(probs: torch.Tensor, min_p: torch.Tensor) -> torch.Tensor:
 
 
 def target_probs(logits: torch.Tensor, *, temperatures, top_ks, top_ps, min_ps,
-                 rows_per_request: int) -> torch.Tensor:
+                 rows_per_request: int, compute_dtype=torch.float32) -> torch.Tensor:
     """Dense ``[B*K, V]`` fp32 target distribution of adjusted logits.
 
     SPEC/dflash_utils.py:743-810 (``build_dflash_verify_target_probs``):
@@ -310,11 +310,14 @@ def target_probs(logits: torch.Tensor, *, temperatures, top_ks, top_ps, min_ps,
     ``SRT/layers/sampler.py:238-242``.
     Per-request parameters are ``[B]`` tensors; ``top_k >= V`` disables top-k,
     ``top_p >= 1`` disables top-p and ``min_p <= 0`` disables min-p.
+    ``compute_dtype``: precision of everything after ``scaled`` (which is
+    always the fp32 quotient the reference computes); float64 gives the exact
+    value of the formula, free of fp32 summation order.  Returned as float32.
     """
     rows, vocab = logits.shape
     k = rows_per_request
     temp = torch.repeat_interleave(temperatures.float().reshape(-1), k)
-    scaled = logits.float() / temp[:, None]
+    scaled = (logits.float() / temp[:, None]).to(compute_dtype)
     top_k_rows = torch.repeat_interleave(top_ks.to(torch.int64).reshape(-1), k).clamp(1, vocab)
     top_p_rows = torch.repeat_interleave(top_ps.float().reshape(-1), k)
     min_p_rows = torch.repeat_interleave(min_ps.float().reshape(-1), k)
@@ -326,17 +329,17 @@ def target_probs(logits: torch.Tensor, *, temperatures, top_ks, top_ps, min_ps,
         vals = vals.masked_fill(ranks >= top_k_rows[:, None], float("-inf"))
         probs_k = torch.softmax(vals, dim=-1)
         if need_top_p:
-            probs_k = top_p_renorm(probs_k, top_p_rows)
-        dense = torch.zeros(rows, vocab, dtype=torch.float32)
+            probs_k = top_p_renorm(probs_k, top_p_rows.to(compute_dtype))
+        dense = torch.zeros(rows, vocab, dtype=compute_dtype)
         dense.scatter_(1, idx, probs_k)
     else:
         dense = torch.softmax(scaled, dim=-1)
         if need_top_p:
             sorted_p, order = torch.sort(dense, dim=-1, descending=True, stable=True)
-            dense = torch.zeros_like(dense).scatter_(1, order, top_p_renorm(sorted_p, top_p_rows))
+            dense = torch.zeros_like(dense).scatter_(1, order, top_p_renorm(sorted_p, top_p_rows.to(compute_dtype)))
     if bool((min_p_rows > 0).any()):
-        dense = min_p_renorm(dense, min_p_rows)
-    return dense
+        dense = min_p_renorm(dense, min_p_rows.to(compute_dtype))
+    return dense.float()
 
 
 # --------------------------------------------------------------------------
