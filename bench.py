@@ -21,6 +21,7 @@ import os
 import statistics
 import sys
 import time
+from types import SimpleNamespace
 
 import torch
 
@@ -469,8 +470,128 @@ class HbmCopy:
                 "sample": f"128 MiB host copy, median of {n} runs"}
 
 
+class ChainSampling:
+    """chain_speculative_sampling_triton on dense fp32 target [B, K, V] and
+    draft [B, K-1, V] probabilities (softmax of N(0, 3^2) logits at T 0.8,
+    drafted tokens drawn from q), batch 128 x block 16."""
+
+    name = "chain_sampling"
+    metric = "dense-q chain sampling GB/s (algorithmic bytes) at 128x16x151936 fp32 probabilities"
+    unit = "GB/s"
+    dtype = "f32"
+
+    def __init__(self, dev, batch=128, width=16, vocab=V):
+        from longspark_amd import accept
+        g = torch.Generator(device=dev).manual_seed(81)
+        self.batch, self.width, self.vocab = batch, width, vocab
+        x = 3.0 * torch.randn(batch, width, vocab, generator=g, device=dev)
+        self.p = torch.softmax(x / 0.8, dim=-1)
+        x[:, :width - 1] += torch.randn(batch, width - 1, vocab, generator=g, device=dev)
+        self.q = torch.softmax(x[:, :width - 1] / 0.8, dim=-1)
+        del x
+        self.cand = torch.zeros(batch, width, dtype=torch.int64, device=dev)
+        self.cand[:, 1:] = torch.multinomial(self.q.reshape(-1, vocab), 1, generator=g).view(batch, width - 1)
+        self.u = torch.rand(batch, width - 1, generator=g, device=dev)
+        self.uf = torch.rand(batch, generator=g, device=dev)
+        (self.ridx, self.nxt, self.sib, self.predicts, self.aidx,
+         self.anum) = accept.chain_verify_buffers(bs=batch, draft_token_num=width, device=dev)
+        self.bytes = batch * vocab * 4 * 2   # until count_rejected: p and q rows for every request
+        self.units = self.bytes / 1e9
+        self.kernel = "chain_kernel"
+
+    def step(self):
+        from longspark_amd import accept
+        accept.chain_speculative_sampling_triton(
+            self.predicts, self.aidx, self.anum, self.cand, self.ridx, self.nxt, self.sib, self.u, self.uf,
+            self.p, self.q, 1.0, 1.0, True)
+        return self.anum
+
+    def count_rejected(self, anum):
+        """Algorithmic bytes: per request the drafted tokens' p and q up to the
+        first rejection, the bonus row of p, and q's row after a rejection."""
+        n = anum.long().cpu()
+        rejected = int((n < self.width - 1).sum())
+        gathered = int((torch.clamp(n + 1, max=self.width - 1)).sum()) * 8
+        self.bytes = self.batch * self.vocab * 4 + rejected * self.vocab * 4 + gathered
+        self.units = self.bytes / 1e9
+        self.rejected = rejected
+
+    def config(self):
+        return {"workload": f"chain sampling B={self.batch} K={self.width} V={self.vocab} fp32 p and q",
+                "batch": self.batch, "block": self.width, "vocab": self.vocab,
+                "rejected_requests": getattr(self, "rejected", None)}
+
+    def cpu_baseline(self, threads):
+        from oracle import verify as ov
+        torch.set_num_threads(threads)
+        b = 8
+        p, q = self.p[:b].cpu(), self.q[:b].cpu()
+        cand, u, uf = self.cand[:b].cpu(), self.u[:b].cpu(), self.uf[:b].cpu()
+        med, n = time_cpu(lambda: ov.chain_speculative_sampling(candidates=cand, uniform_samples=u, uniform_final=uf,
+                                                                 target_probs_3d=p, draft_probs_3d=q))
+        return {"value": b * self.vocab * 8 / med / 1e9, "threads": threads,
+                "sample": f"{b} requests, oracle torch-CPU chain sampling, median of {n} runs"}
+
+
+class _BatchInfo(SimpleNamespace):
+    """The sampling-info fields the verify logit adjustments read (one entry per request)."""
+
+    def __len__(self):
+        return self.temperatures.shape[0]
+
+
+class AdjustLogits:
+    """apply_dflash_verify_logits_adjustments (overlap path): fp32
+    acc_linear_penalties and logit_bias [B, V] added in bf16 to every row of
+    each request, in place on [B*K, V] bf16 logits, batch 128 x block 16."""
+
+    name = "adjust_logits"
+    metric = "verify logit adjustments GB/s (algorithmic bytes) at 128x16x151936 bf16"
+    unit = "GB/s"
+    dtype = "bf16"
+
+    def __init__(self, dev, batch=128, width=16, vocab=V):
+        from longspark_amd import workloads
+        self.batch, self.width, self.vocab = batch, width, vocab
+        self.logits, _ = workloads.greedy_inputs(batch, width, vocab, seed=82, device=dev, gen_device=dev)
+        g = torch.Generator(device=dev).manual_seed(83)
+        acc = -0.05 * torch.randint(0, 3, (batch, vocab), generator=g, device=dev).float()
+        lb = torch.zeros(batch, vocab, device=dev)
+        lb[:, ::101] = 0.01
+        self.info = _BatchInfo(acc_linear_penalties=acc, logit_bias=lb, penalizer_orchestrator=None,
+                               vocab_mask=None, has_custom_logit_processor=False,
+                               temperatures=torch.ones(batch, 1, device=dev))
+        rows = batch * width
+        self.bytes = rows * vocab * 2 * 2 + 2 * batch * vocab * 4   # logits read + written, two fp32 [B, V]
+        self.units = self.bytes / 1e9
+        self.kernel = "request_bias_kernel"
+
+    def step(self):
+        from longspark_amd import penalties
+        penalties.apply_dflash_verify_logits_adjustments(next_token_logits=self.logits, sampling_info=self.info,
+                                                         draft_token_num=self.width)
+
+    def config(self):
+        return {"workload": f"verify logit adjustments B={self.batch} K={self.width} V={self.vocab} bf16",
+                "batch": self.batch, "block": self.width, "vocab": self.vocab}
+
+    def cpu_baseline(self, threads):
+        torch.set_num_threads(threads)
+        b = 4
+        x = self.logits[:b * self.width].cpu().view(b, self.width, self.vocab)
+        acc = self.info.acc_linear_penalties[:b].cpu()
+        lb = self.info.logit_bias[:b].cpu()
+
+        def run():  # the reference's tensor operations (dflash_utils.py:193-213) on the CPU
+            x.add_(acc.to(x.dtype)[:, None, :])
+            x.add_(lb.to(x.dtype)[:, None, :])
+        med, n = time_cpu(run)
+        return {"value": (b * self.width * self.vocab * 4 + 2 * b * self.vocab * 4) / med / 1e9,
+                "threads": threads, "sample": f"{b} requests, torch-CPU adds of the reference, median of {n} runs"}
+
+
 WORKLOADS = {w.name: w for w in (GreedyVerify, StochasticVerify, WindowGather, SummaryUpdate, SoftmaxTempWorkload,
-                                  TargetProbsWorkload, HbmCopy)}
+                                  TargetProbsWorkload, ChainSampling, AdjustLogits, HbmCopy)}
 DEFAULT_WORKLOAD = "verify_sample"
 
 

@@ -81,7 +81,7 @@ LS_API const char* ls_version(void);
  * cutoff_verify_lens (int32 [batch], may be NULL): per-request verify window;
  *   the accepted length is capped at cutoff_verify_lens[b] - 1 and the number
  *   of tokens cut is written to cap_trim[b] (int32, may be NULL), as
- *   SRT/speculative/dspark_components/kernels/cap_correct_len.py:39-47 does
+ *   SRT/speculative/dspark_components/kernels/cap_correct_len.py:44-52 does
  *   (the capped length is clamped to [0, width-1] for memory safety).
  * Outputs: accept_lens[b] (int32) = number of accepted drafted tokens,
  *   bonus[b] (int64) = argmax of row accept_lens[b],
@@ -149,6 +149,26 @@ LS_API int ls_adjust_logits(void* logits, int32_t logits_dtype, int64_t row_stri
                             int64_t pen_words_stride, const float* pen_add, int64_t pen_add_stride,
                             const float* repetition, int32_t verify_quirk, const int32_t* vocab_mask,
                             int64_t mask_stride, int32_t mask_rows_per_request, int64_t mask_words, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Per-request bias vectors added in place to every row of the request:
+ * replaces the additions of SRT/speculative/dflash_utils.py:176-213
+ * (apply_dflash_verify_logits_adjustments with the caller's dense [B, V]
+ * penalty, mask and logit-bias tensors).
+ * logits [rows, vocab] (fp32/bf16/fp16; row r belongs to request
+ * r / rows_per_request); bias, bias2: fp32 [rows / rows_per_request, vocab]
+ * (row strides bias_stride, bias2_stride; either may be NULL);
+ * vocab_mask: packed int32 [rows / rows_per_request, mask_words] (may be NULL).
+ *   separate = 0 (:176-191): z = bias (0 when NULL), columns v < 32*mask_words
+ *     whose mask bit (LSB first) is 0 become -inf, then z += bias2; every row
+ *     of the request gets l = T(l + T(z)), T = rounding to the logits' dtype.
+ *   separate = 1 (:193-213, no mask): l = T(l + T(bias)), then
+ *     l = T(l + T(bias2)); a NULL tensor is not added.
+ * ------------------------------------------------------------------------- */
+LS_API int ls_add_request_bias(void* logits, int32_t logits_dtype, int64_t row_stride, int64_t rows, int64_t vocab,
+                               int32_t rows_per_request, const float* bias, int64_t bias_stride,
+                               const int32_t* vocab_mask, int64_t mask_stride, int64_t mask_words,
+                               const float* bias2, int64_t bias2_stride, int32_t separate, void* stream);
 
 /* ---------------------------------------------------------------------------
  * Fused stochastic chain verification of a drafted block.
@@ -247,6 +267,14 @@ typedef struct {
    * row is top-k with repetition >= 1 and additive penalties <= 0; other rows
    * are still resolved exactly, more slowly), 2 = only the exact scan. */
   int32_t scan_hint;
+  /* Optional verify-length cutoff (SRT/speculative/dspark_components/kernels/
+   * cap_correct_len.py:44-52 applied as accept_sampling.py:151-157,185-186 does):
+   * cutoff_verify_lens [batch] int32 or NULL; accept_lens[b] becomes
+   * min(accepted, max(cutoff - 1, 0)), cap_trim[b] (int32, may be NULL) the
+   * drafted tokens removed, and a capped request's bonus is its drafted
+   * token at the cap. */
+  const int32_t* cutoff_verify_lens;
+  int32_t* cap_trim;
 } ls_verify_sample_args;
 
 LS_API int ls_verify_sample_workspace(int64_t batch, int32_t width, int64_t vocab, int32_t max_top_k,
@@ -324,6 +352,60 @@ LS_API int ls_decide_acceptance(const void* candidates, int32_t candidates_dtype
 LS_API int ls_finish_sampling(const float* target_rows, int64_t rows_stride_b, const int64_t* rejected_rows,
                               int64_t n_rejected, const float* rejected_q_rows, int64_t q_stride_b,
                               const float* uniforms, int64_t batch, int64_t vocab, int64_t* tokens, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Dense-q chain rejection sampling: replaces
+ * SRT/speculative/reject_sampling.py:159-204 (chain_speculative_sampling_triton
+ * and its kernel :5-156) for the chain layout of
+ * SRT/speculative/dflash_utils.py:216-272.
+ * target_probs [batch, width, vocab] and draft_probs [batch, width-1, vocab]
+ * fp32 with unit vocabulary stride; candidates and retrive_index
+ * [batch, width] int32/int64; uniforms [batch, width-1] (unit column stride),
+ * final_uniforms [batch].
+ * Drafted token j = candidates[b, j+1] is accepted while
+ * uniforms[b, j] * draft_probs[b, j, tok] < target_probs[b, j, tok]; with L
+ * accepted, the bonus is drawn from max(p - q, 0) at row L (p at row L when
+ * L = width-1): the first token whose running sum exceeds
+ * final_uniforms[b] * total, vocab-1 when none does.
+ * Outputs: accept_token_num[b] = L; for n <= L, accept_index[b, n] =
+ * retrive_index[b, n] and predicts[retrive_index[b, n]] = candidates[b, n+1]
+ * (n < L) or the bonus (n = L); other entries are left as they are.
+ * predicts must hold every retrive_index value.  Running sums are fp64.
+ * Workspace sizes from ls_chain_sampling_workspace; the counters must be zero
+ * on entry and are zero again when the call's work ends.
+ * ------------------------------------------------------------------------- */
+typedef struct {
+  const float* target_probs;
+  int64_t tp_stride_b;
+  int64_t tp_stride_k;
+  const float* draft_probs;
+  int64_t dp_stride_b;
+  int64_t dp_stride_k;
+  const void* candidates;
+  int32_t candidates_dtype;
+  int64_t cand_stride_b;
+  int64_t cand_stride_k;
+  const void* retrive_index;
+  int32_t retrive_index_dtype;
+  int64_t ri_stride_b;
+  int64_t ri_stride_k;
+  const float* uniforms;
+  int64_t uniform_stride_b;
+  const float* final_uniforms;
+  int64_t batch;
+  int32_t width;
+  int64_t vocab;
+  int32_t* predicts;
+  int32_t* accept_index;
+  int64_t ai_stride_b;
+  int64_t ai_stride_k;
+  int32_t* accept_token_num;
+} ls_chain_sampling_args;
+
+LS_API int ls_chain_sampling_workspace(int64_t batch, int64_t vocab, uint64_t* counter_bytes,
+                                       uint64_t* scratch_bytes);
+LS_API int ls_chain_speculative_sampling(const ls_chain_sampling_args* args, void* counters, uint64_t counter_bytes,
+                                         void* scratch, uint64_t scratch_bytes, void* stream);
 
 /* Fixed-width verify outputs: out_tokens[b, c] = bonus[b] if c == accept_lens[b],
  * else candidates[b, c+1] (0 in the last column); committed[b] = accept_lens[b] + 1

@@ -54,6 +54,7 @@ class VerifySampleArgs(ctypes.Structure):
         ("uniforms", P), ("uniform_stride_b", I64), ("final_uniforms", P),
         ("accept_lens", P), ("bonus", P), ("p_cand_out", P), ("status", P),
         ("timing_events", P), ("scan_hint", I32),
+        ("cutoff_verify_lens", P), ("cap_trim", P),
     ]
 
 
@@ -64,6 +65,20 @@ class TargetProbsArgs(ctypes.Structure):
         ("batch", I64), ("rows_per_request", I32), ("vocab", I64),
         ("temperatures", P), ("top_ks", P), ("top_ps", P), ("min_ps", P), ("max_top_k", I32),
         ("out", P), ("out_row_stride", I64), ("status", P), ("scan_hint", I32),
+    ]
+
+
+class ChainSamplingArgs(ctypes.Structure):
+    """Mirror of ``ls_chain_sampling_args``."""
+    _fields_ = [
+        ("target_probs", P), ("tp_stride_b", I64), ("tp_stride_k", I64),
+        ("draft_probs", P), ("dp_stride_b", I64), ("dp_stride_k", I64),
+        ("candidates", P), ("candidates_dtype", I32), ("cand_stride_b", I64), ("cand_stride_k", I64),
+        ("retrive_index", P), ("retrive_index_dtype", I32), ("ri_stride_b", I64), ("ri_stride_k", I64),
+        ("uniforms", P), ("uniform_stride_b", I64), ("final_uniforms", P),
+        ("batch", I64), ("width", I32), ("vocab", I64),
+        ("predicts", P), ("accept_index", P), ("ai_stride_b", I64), ("ai_stride_k", I64),
+        ("accept_token_num", P),
     ]
 
 
@@ -101,6 +116,7 @@ _SIGNATURES = {
                                P, U64, P, U64, P]),
     "ls_penalty_tables": (I32, [P, I64, P, I64, I32, I64, P, P, P, P, I64, P, I64, P, P, P]),
     "ls_adjust_logits": (I32, [P, I32, I64, I64, I64, I32, P, P, I64, P, I64, P, I32, P, I64, I32, I64, P]),
+    "ls_add_request_bias": (I32, [P, I32, I64, I64, I64, I32, P, I64, P, I64, I64, P, I64, I32, P]),
     "ls_verify_sample_workspace": (I32, [I64, I32, I64, I32, P, P]),
     "ls_verify_sample": (I32, [ctypes.POINTER(VerifySampleArgs), P, U64, P, U64, P]),
     "ls_softmax_temp": (I32, [P, I32, I64, I64, I64, P, I32, P, I64, P]),
@@ -108,6 +124,8 @@ _SIGNATURES = {
     "ls_target_probs": (I32, [ctypes.POINTER(TargetProbsArgs), P, U64, P, U64, P]),
     "ls_decide_acceptance": (I32, [P, I32, I64, I64, P, I64, P, I64, P, I64, I64, I64, I32, I64, P, P, I64, P]),
     "ls_finish_sampling": (I32, [P, I64, P, I64, P, I64, P, I64, I64, P, P]),
+    "ls_chain_sampling_workspace": (I32, [I64, I64, P, P]),
+    "ls_chain_speculative_sampling": (I32, [ctypes.POINTER(ChainSamplingArgs), P, U64, P, U64, P]),
     "ls_finalize_verify_outputs": (I32, [P, I32, I64, I64, P, I32, I64, P, I32, I64, P, I32, I64, I64, I32, P, P, P,
                                          P]),
     "ls_raw_page_table": (I32, [P, I64, I64, P, I32, P, I32, I64, I32, P, I64, P, P]),

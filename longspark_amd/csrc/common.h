@@ -216,6 +216,12 @@ __device__ __forceinline__ uint64_t atomic_take_u64(uint64_t* p) {
 __device__ __forceinline__ uint32_t atomic_take_u32(uint32_t* p) {
   return __hip_atomic_exchange(p, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// Publish a word with an atomic exchange; the returned old value is kept
+// live so that a later wait for outstanding loads covers the exchange.
+__device__ __forceinline__ void atomic_put_u64(uint64_t* p, uint64_t v) {
+  uint64_t old = __hip_atomic_exchange(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  asm volatile("" ::"v"(old));
+}
 // Current value of a word published by atomic RMWs: an agent-scope atomic
 // load (a coherent load, served from the coherence point and not from a
 // stale line of the reader's L2), which leaves the word unchanged.

@@ -135,6 +135,86 @@ __global__ __launch_bounds__(kPT) void adjust_logits_kernel(
   }
 }
 
+// Per-request bias vectors added to every row of the request, in the logits'
+// dtype (SRT/speculative/dflash_utils.py:176-213):
+//   separate == 0 (the dense path, :176-191): z = bias (0 when absent), then
+//     columns whose mask bit is 0 become -inf (the grammar mask fills the bias
+//     tensor), then z += bias2; each row gets l = T(l + T(z)).
+//   separate == 1 (:193-213): l = T(l + T(bias)), then l = T(l + T(bias2)).
+// T(x) is the rounding to the logits' dtype (the reference converts the fp32
+// tensor with .to(dtype) and adds in that dtype: fp32 sum, one rounding).
+// One thread owns 4 columns of one request: it reads the bias columns once
+// and applies them to all rows_per_request rows.
+constexpr int kRB = 256;
+
+template <typename T, bool kVec>
+__global__ __launch_bounds__(kRB) void request_bias_kernel(
+    T* __restrict__ logits, int64_t row_stride, int64_t vocab, int rows_per_request,
+    const float* __restrict__ bias, int64_t bias_stride, const uint32_t* __restrict__ mask, int64_t mask_stride,
+    int64_t mask_vocab, const float* __restrict__ bias2, int64_t bias2_stride, int separate) {
+  const int64_t b = blockIdx.y;
+  const int64_t v0 = (static_cast<int64_t>(blockIdx.x) * kRB + threadIdx.x) * 4;
+  if (v0 >= vocab) return;
+  const int n = static_cast<int>(min<int64_t>(4, vocab - v0));
+  float z1[4], z2[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int64_t v = v0 + e;
+    float a = 0.f, c = 0.f;
+    if (e < n) {
+      if (bias) a = bias[b * bias_stride + v];
+      if (bias2) c = bias2[b * bias2_stride + v];
+      if (!separate && mask && v < mask_vocab && !((mask[b * mask_stride + (v >> 5)] >> (v & 31)) & 1u))
+        a = -INFINITY;
+    }
+    if (separate) {
+      z1[e] = to_f32<T>(from_f32<T>(a));
+      z2[e] = to_f32<T>(from_f32<T>(c));
+    } else {
+      z1[e] = to_f32<T>(from_f32<T>(a + c));
+    }
+  }
+  T* rp = logits + b * rows_per_request * row_stride + v0;
+  for (int j = 0; j < rows_per_request; ++j, rp += row_stride) {
+    T x[4];
+    if (kVec && n == 4) {
+      if constexpr (sizeof(T) == 4) {
+        const float4 t = *reinterpret_cast<const float4*>(rp);
+        x[0] = t.x; x[1] = t.y; x[2] = t.z; x[3] = t.w;
+      } else {
+        const uint2 t = *reinterpret_cast<const uint2*>(rp);
+        __builtin_memcpy(x, &t, 8);
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (e < n) x[e] = rp[e];
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if (!separate) {
+        x[e] = from_f32<T>(to_f32<T>(x[e]) + z1[e]);
+      } else {  // an absent tensor is not added (it would turn -0 into +0)
+        if (bias) x[e] = from_f32<T>(to_f32<T>(x[e]) + z1[e]);
+        if (bias2) x[e] = from_f32<T>(to_f32<T>(x[e]) + z2[e]);
+      }
+    }
+    if (kVec && n == 4) {
+      if constexpr (sizeof(T) == 4) {
+        *reinterpret_cast<float4*>(rp) = make_float4(x[0], x[1], x[2], x[3]);
+      } else {
+        uint2 t;
+        __builtin_memcpy(&t, x, 8);
+        *reinterpret_cast<uint2*>(rp) = t;
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (e < n) rp[e] = x[e];
+    }
+  }
+}
+
 }  // namespace
 }  // namespace ls
 
@@ -190,6 +270,49 @@ extern "C" int ls_adjust_logits(void* logits, int32_t logits_dtype, int64_t row_
   else if (logits_dtype == LS_F16) LS_ADJ(__half);
   else return fail(LS_ERR_DTYPE, "ls_adjust_logits: logits must be fp32, bf16 or fp16");
 #undef LS_ADJ
+  LS_LAUNCH_CHECK();
+  return LS_OK;
+}
+
+extern "C" int ls_add_request_bias(void* logits, int32_t logits_dtype, int64_t row_stride, int64_t rows,
+                                   int64_t vocab, int32_t rows_per_request, const float* bias, int64_t bias_stride,
+                                   const int32_t* vocab_mask, int64_t mask_stride, int64_t mask_words,
+                                   const float* bias2, int64_t bias2_stride, int32_t separate, void* stream) {
+  using namespace ls;
+  LS_CHECK(logits, LS_ERR_VALUE, "ls_add_request_bias: null logits");
+  LS_CHECK(rows > 0 && vocab > 0 && rows_per_request > 0 && rows % rows_per_request == 0, LS_ERR_SHAPE,
+           "ls_add_request_bias: rows must be a positive multiple of rows_per_request");
+  LS_CHECK(row_stride >= vocab, LS_ERR_SHAPE, "ls_add_request_bias: row stride < vocab");
+  const int64_t batch = rows / rows_per_request;
+  LS_CHECK(batch <= 65535, LS_ERR_SHAPE, "ls_add_request_bias: at most 65535 requests per call");
+  LS_CHECK((!bias || bias_stride >= vocab) && (!bias2 || bias2_stride >= vocab), LS_ERR_SHAPE,
+           "ls_add_request_bias: bias stride < vocab");
+  LS_CHECK(!vocab_mask || (mask_words > 0 && mask_stride >= mask_words), LS_ERR_SHAPE,
+           "ls_add_request_bias: bad mask shape");
+  LS_CHECK(!(separate && vocab_mask), LS_ERR_VALUE, "ls_add_request_bias: the mask belongs to the combined form");
+  if (!bias && !bias2 && !vocab_mask) return LS_OK;
+  const int64_t mask_vocab = vocab_mask ? (mask_words * 32 < vocab ? mask_words * 32 : vocab) : 0;
+  const dim3 grid(static_cast<unsigned>((vocab + kRB * 4 - 1) / (kRB * 4)), static_cast<unsigned>(batch));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const uint32_t* m = reinterpret_cast<const uint32_t*>(vocab_mask);
+#define LS_RB(T)                                                                                               \
+  do {                                                                                                         \
+    T* lp = static_cast<T*>(logits);                                                                           \
+    const bool vec = ((reinterpret_cast<uintptr_t>(lp) % (4 * sizeof(T))) == 0) && row_stride % 4 == 0;       \
+    if (vec)                                                                                                   \
+      request_bias_kernel<T, true><<<grid, kRB, 0, s>>>(lp, row_stride, vocab, rows_per_request, bias,         \
+                                                         bias_stride, m, mask_stride, mask_vocab, bias2,       \
+                                                         bias2_stride, separate);                              \
+    else                                                                                                       \
+      request_bias_kernel<T, false><<<grid, kRB, 0, s>>>(lp, row_stride, vocab, rows_per_request, bias,        \
+                                                          bias_stride, m, mask_stride, mask_vocab, bias2,      \
+                                                          bias2_stride, separate);                             \
+  } while (0)
+  if (logits_dtype == LS_F32) LS_RB(float);
+  else if (logits_dtype == LS_BF16) LS_RB(uint16_t);
+  else if (logits_dtype == LS_F16) LS_RB(__half);
+  else return fail(LS_ERR_DTYPE, "ls_add_request_bias: logits must be fp32, bf16 or fp16");
+#undef LS_RB
   LS_LAUNCH_CHECK();
   return LS_OK;
 }

@@ -11,6 +11,13 @@
 //             column), committed = L+1, next = prefix + L + 1
 //             (SRT/speculative/draft_free_kv_dispatch.py:8-57,
 //              SRT/speculative/draft_free_kv_utils.py:386-408)
+//   chain     dense-q chain rejection sampling: accept drafted token j while
+//             u[b,j] * q[b,j,c] < p[b,j,c] (c = cand[b, j+1]); the bonus is the
+//             first v whose running sum of max(p - q, 0) at the first
+//             rejection (p itself when all are accepted) exceeds
+//             u_final * total, V-1 when none does; outputs in the
+//             predicts / accept_index / accept_token_num layout
+//             (SRT/speculative/reject_sampling.py:5-204)
 // SRT = vendor/sglang/python/sglang/srt.
 #include "common.h"
 
@@ -232,7 +239,222 @@ __global__ __launch_bounds__(kST) void finalize_kernel(FinalizeArgs a) {
   }
 }
 
+// ------------------------------------------------------------ chain sampling
+//
+// Several workgroups per request: each sums the bonus row's values over its
+// share of 1024-element chunks (one wave per chunk, fp64 sums) and publishes
+// the chunk sums; the last workgroup to arrive for the request walks the
+// chunk sums to the chunk where the running sum passes u * total and scans
+// that chunk element by element.  The values are fp32 (max(p - q, 0) as the
+// reference forms them); the running sums are fp64.
+
+constexpr int kCT = 256;        // threads per chain workgroup
+constexpr int kCChunk = 1024;   // elements per chunk: 16 per lane of one wave
+constexpr int kCWaves = kCT / kWave;
+
+struct ChainArgs {
+  const float* p;
+  int64_t psb, psk;
+  const float* q;
+  int64_t qsb, qsk;
+  const void* cand;
+  int cand_dtype;
+  int64_t csb, csk;
+  const void* ridx;
+  int ridx_dtype;
+  int64_t rsb, rsk;
+  const float* u;
+  int64_t usb;
+  const float* uf;
+  int64_t batch;
+  int width;
+  int64_t vocab;
+  int32_t* predicts;
+  int32_t* aidx;
+  int64_t aisb, aisk;
+  int32_t* anum;
+  uint64_t* part;     // [batch, nchunks] chunk sums (fp64 bit patterns)
+  uint32_t* arrive;   // [batch] arrivals (zero between calls)
+  int64_t nchunks;
+  int slices, cps;    // workgroups per request, chunks per workgroup
+};
+
+__device__ __forceinline__ double wave_incl_scan_d(double v) {
+  const int lane = threadIdx.x & (kWave - 1);
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const double t = __shfl_up(v, o, kWave);
+    if (lane >= o) v += t;
+  }
+  return v;
+}
+
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+  for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+// Accepted drafts of request b (every lane returns it): drafted token j
+// (candidates column j + 1) is accepted while u[b, j] * q[b, j, c] < p[b, j, c]
+// (reject_sampling.py:53-88); a token outside [0, vocab) is a rejection.
+__device__ int chain_accept_len(const ChainArgs& a, int64_t b) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int g = a.width - 1;
+  for (int base = 0; base < g; base += kWave) {
+    const int j = base + lane;
+    bool ok = false;
+    if (j < g) {
+      const int64_t c = ld_idx(a.cand, a.cand_dtype, b * a.csb + static_cast<int64_t>(j + 1) * a.csk);
+      if (c >= 0 && c < a.vocab) {
+        const float pj = a.p[b * a.psb + static_cast<int64_t>(j) * a.psk + c];
+        const float qj = a.q[b * a.qsb + static_cast<int64_t>(j) * a.qsk + c];
+        ok = a.u[b * a.usb + j] * qj < pj;
+      }
+    }
+    const uint64_t fail = __ballot(j < g && !ok);
+    if (fail) return base + __ffsll(static_cast<long long>(fail)) - 1;
+  }
+  return g;
+}
+
+// Lane's 16 values of chunk c: x[4 * i + e] is element c * 1024 + i * 256 +
+// lane * 4 + e (0 beyond the vocabulary).  q == nullptr: the values are p;
+// otherwise max(p - q, 0) (NaN differences count as 0, reject_sampling.py:103-107).
+template <bool kVec>
+__device__ __forceinline__ void chain_chunk(const float* __restrict__ p, const float* __restrict__ q, int64_t vocab,
+                                            int64_t c, float* x) {
+  const int lane = threadIdx.x & (kWave - 1);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t v0 = c * kCChunk + i * (kWave * 4) + lane * 4;
+    float pv[4], qv[4] = {0.f, 0.f, 0.f, 0.f};
+    if (kVec && v0 + 3 < vocab) {
+      const float4 t = *reinterpret_cast<const float4*>(p + v0);
+      pv[0] = t.x; pv[1] = t.y; pv[2] = t.z; pv[3] = t.w;
+      if (q) {
+        const float4 d = *reinterpret_cast<const float4*>(q + v0);
+        qv[0] = d.x; qv[1] = d.y; qv[2] = d.z; qv[3] = d.w;
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        pv[e] = v0 + e < vocab ? p[v0 + e] : 0.f;
+        if (q) qv[e] = v0 + e < vocab ? q[v0 + e] : 0.f;
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float d = pv[e] - qv[e];
+      x[4 * i + e] = q ? (d > 0.f ? d : 0.f) : pv[e];
+    }
+  }
+}
+
+template <bool kVec>
+__global__ __launch_bounds__(kCT) void chain_kernel(ChainArgs a) {
+  __shared__ int s_last;
+  const int64_t b = static_cast<int64_t>(blockIdx.x) % a.batch;
+  const int slice = static_cast<int>(static_cast<int64_t>(blockIdx.x) / a.batch);
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1), wid = tid / kWave;
+  const int len = chain_accept_len(a, b);
+  const bool rejected = len < a.width - 1;
+  const float* prow = a.p + b * a.psb + static_cast<int64_t>(len) * a.psk;
+  const float* qrow = rejected ? a.q + b * a.qsb + static_cast<int64_t>(len) * a.qsk : nullptr;
+  uint64_t* part = a.part + b * a.nchunks;
+
+  // chunk sums of this workgroup's share
+  const int64_t c_end = min<int64_t>(a.nchunks, static_cast<int64_t>(slice + 1) * a.cps);
+  for (int64_t c = static_cast<int64_t>(slice) * a.cps + wid; c < c_end; c += kCWaves) {
+    float x[16];
+    chain_chunk<kVec>(prow, qrow, a.vocab, c, x);
+    double t = 0.0;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) t += static_cast<double>(x[k]);
+    t = wave_sum_d(t);
+    if (lane == 0) atomic_put_u64(part + c, static_cast<uint64_t>(__double_as_longlong(t)));
+  }
+  __syncthreads();
+  if (tid == 0) s_last = arrive(a.arrive + b) == static_cast<uint32_t>(a.slices - 1) ? 1 : 0;
+  __syncthreads();
+  if (!s_last || wid != 0) return;
+  if (lane == 0) atomic_take_u32(a.arrive + b);  // back to zero for the next call
+
+  // The last workgroup: total, then the chunk where the running sum passes
+  // u * total (both walks use the same group-wise scan, so they agree).
+  auto chunk_sum = [&](int64_t c) -> double {
+    return c < a.nchunks ? __longlong_as_double(static_cast<long long>(atomic_peek_u64(part + c))) : 0.0;
+  };
+  double total = 0.0;
+  for (int64_t c0 = 0; c0 < a.nchunks; c0 += kWave) {
+    const double inc = wave_incl_scan_d(chunk_sum(c0 + lane));
+    total += __shfl(inc, kWave - 1, kWave);
+  }
+  const double target = static_cast<double>(a.uf[b]) * total;
+  int64_t hit_chunk = -1;
+  double base = 0.0;
+  for (int64_t c0 = 0; c0 < a.nchunks; c0 += kWave) {
+    const double x = chunk_sum(c0 + lane);
+    const double inc = wave_incl_scan_d(x);
+    const uint64_t m = __ballot(c0 + lane < a.nchunks && base + inc > target);
+    if (m) {
+      const int l = __ffsll(static_cast<long long>(m)) - 1;
+      hit_chunk = c0 + l;
+      base += __shfl(inc - x, l, kWave);
+      break;
+    }
+    base += __shfl(inc, kWave - 1, kWave);
+  }
+  int64_t tok = a.vocab - 1;
+  if (hit_chunk >= 0) {
+    float x[16];
+    chain_chunk<kVec>(prow, qrow, a.vocab, hit_chunk, x);
+    int64_t found = -1, last_pos = -1;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      double ls = 0.0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ls += static_cast<double>(x[4 * i + e]);
+      const double inc = wave_incl_scan_d(ls);
+      double run = base + (inc - ls);
+      int first = -1, lastpos = -1;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        run += static_cast<double>(x[4 * i + e]);
+        if (first < 0 && run > target) first = e;
+        if (x[4 * i + e] > 0.f) lastpos = e;
+      }
+      const int64_t v0 = hit_chunk * kCChunk + i * (kWave * 4) + lane * 4;
+      const uint64_t m = __ballot(found < 0 && first >= 0);
+      if (found < 0 && m) {
+        const int l = __ffsll(static_cast<long long>(m)) - 1;
+        found = __shfl(v0 + first, l, kWave);
+      }
+      const uint64_t mp = __ballot(lastpos >= 0);
+      if (mp) {
+        const int l = 63 - __clzll(static_cast<long long>(mp));
+        last_pos = __shfl(v0 + lastpos, l, kWave);
+      }
+      base += __shfl(inc, kWave - 1, kWave);
+    }
+    // the running sum passed the target inside this chunk up to rounding:
+    // without an element past it, the chunk's last positive element
+    tok = found >= 0 ? found : (last_pos >= 0 ? last_pos : a.vocab - 1);
+  }
+  for (int n = lane; n <= len; n += kWave) {
+    const int64_t slot = ld_idx(a.ridx, a.ridx_dtype, b * a.rsb + static_cast<int64_t>(n) * a.rsk);
+    a.aidx[b * a.aisb + static_cast<int64_t>(n) * a.aisk] = static_cast<int32_t>(slot);
+    const int64_t t = n < len ? ld_idx(a.cand, a.cand_dtype, b * a.csb + static_cast<int64_t>(n + 1) * a.csk) : tok;
+    a.predicts[slot] = static_cast<int32_t>(t);
+  }
+  if (lane == 0) a.anum[b] = len;
+}
+
 inline bool is_index(int d) { return d == LS_I32 || d == LS_I64; }
+
+inline uint64_t chain_up256(uint64_t x) { return (x + 255) & ~uint64_t(255); }
+inline int64_t chain_chunks(int64_t vocab) { return (vocab + kCChunk - 1) / kCChunk; }
 
 }  // namespace
 }  // namespace ls
@@ -293,6 +515,63 @@ extern "C" int ls_finalize_verify_outputs(const void* candidates, int32_t candid
                  out_tokens, committed, next_lengths};
   const int64_t n = batch * width;
   finalize_kernel<<<dim3(static_cast<unsigned>((n + kST - 1) / kST)), kST, 0, static_cast<hipStream_t>(stream)>>>(a);
+  LS_LAUNCH_CHECK();
+  return LS_OK;
+}
+
+extern "C" int ls_chain_sampling_workspace(int64_t batch, int64_t vocab, uint64_t* counter_bytes,
+                                           uint64_t* scratch_bytes) {
+  using namespace ls;
+  LS_CHECK(batch >= 0 && vocab >= 1, LS_ERR_SHAPE, "ls_chain_sampling_workspace: bad sizes");
+  LS_CHECK(counter_bytes && scratch_bytes, LS_ERR_VALUE, "ls_chain_sampling_workspace: null output");
+  *counter_bytes = chain_up256(4 * static_cast<uint64_t>(batch));
+  *scratch_bytes = chain_up256(8 * static_cast<uint64_t>(batch) * static_cast<uint64_t>(chain_chunks(vocab)));
+  return LS_OK;
+}
+
+extern "C" int ls_chain_speculative_sampling(const ls_chain_sampling_args* args, void* counters,
+                                             uint64_t counter_bytes, void* scratch, uint64_t scratch_bytes,
+                                             void* stream) {
+  using namespace ls;
+  LS_CHECK(args, LS_ERR_VALUE, "ls_chain_speculative_sampling: null args");
+  const ls_chain_sampling_args& x = *args;
+  LS_CHECK(x.batch >= 0 && x.width >= 2 && x.vocab >= 1, LS_ERR_SHAPE,
+           "ls_chain_speculative_sampling: need batch >= 0, width >= 2, vocab >= 1");
+  LS_CHECK(x.batch < (int64_t(1) << 24), LS_ERR_SHAPE, "ls_chain_speculative_sampling: batch too large");
+  LS_CHECK(is_index(x.candidates_dtype) && is_index(x.retrive_index_dtype), LS_ERR_DTYPE,
+           "ls_chain_speculative_sampling: candidates and retrive_index must be int32/int64");
+  if (x.batch == 0) return LS_OK;
+  LS_CHECK(x.target_probs && x.draft_probs && x.candidates && x.retrive_index && x.uniforms &&
+               x.final_uniforms && x.predicts && x.accept_index && x.accept_token_num,
+           LS_ERR_VALUE, "ls_chain_speculative_sampling: null pointer");
+  uint64_t need_c = 0, need_s = 0;
+  ls_chain_sampling_workspace(x.batch, x.vocab, &need_c, &need_s);
+  LS_CHECK(counters && scratch && counter_bytes >= need_c && scratch_bytes >= need_s, LS_ERR_SHAPE,
+           "ls_chain_speculative_sampling: needs %llu counter and %llu scratch bytes",
+           (unsigned long long)need_c, (unsigned long long)need_s);
+  ChainArgs a{};
+  a.p = x.target_probs; a.psb = x.tp_stride_b; a.psk = x.tp_stride_k;
+  a.q = x.draft_probs; a.qsb = x.dp_stride_b; a.qsk = x.dp_stride_k;
+  a.cand = x.candidates; a.cand_dtype = x.candidates_dtype; a.csb = x.cand_stride_b; a.csk = x.cand_stride_k;
+  a.ridx = x.retrive_index; a.ridx_dtype = x.retrive_index_dtype; a.rsb = x.ri_stride_b; a.rsk = x.ri_stride_k;
+  a.u = x.uniforms; a.usb = x.uniform_stride_b; a.uf = x.final_uniforms;
+  a.batch = x.batch; a.width = x.width; a.vocab = x.vocab;
+  a.predicts = x.predicts; a.aidx = x.accept_index; a.aisb = x.ai_stride_b; a.aisk = x.ai_stride_k;
+  a.anum = x.accept_token_num;
+  a.arrive = static_cast<uint32_t*>(counters);
+  a.part = static_cast<uint64_t*>(scratch);
+  a.nchunks = chain_chunks(x.vocab);
+  // about 2048 workgroups in all, each with at least one chunk
+  int64_t slices = (2048 + x.batch - 1) / x.batch;
+  if (slices > a.nchunks) slices = a.nchunks;
+  a.cps = static_cast<int>((a.nchunks + slices - 1) / slices);
+  a.slices = static_cast<int>((a.nchunks + a.cps - 1) / a.cps);
+  const bool vec = aligned16(x.target_probs) && aligned16(x.draft_probs) && x.tp_stride_b % 4 == 0 &&
+                   x.tp_stride_k % 4 == 0 && x.dp_stride_b % 4 == 0 && x.dp_stride_k % 4 == 0;
+  const dim3 grid(static_cast<unsigned>(x.batch * a.slices));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (vec) chain_kernel<true><<<grid, kCT, 0, st>>>(a);
+  else chain_kernel<false><<<grid, kCT, 0, st>>>(a);
   LS_LAUNCH_CHECK();
   return LS_OK;
 }

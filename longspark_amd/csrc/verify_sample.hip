@@ -81,6 +81,9 @@ struct Args {
   int64_t* bonus;
   float* p_cand_out;  // [B, K-1] or null
   int32_t* status;    // [1] or null: OR of row flags that blocked a request
+  const int32_t* cutoff;  // [B] verify lengths or null: accepted length capped at cutoff - 1
+  int32_t* trim;          // [B] or null: accepted drafts removed by the cap
+  int cand_i64;           // candidates are int64 (else int32)
   // workspace
   uint32_t* cnt_t;    // [B*K]
   uint32_t* cnt_d;    // [B]
@@ -114,11 +117,6 @@ struct CandRec {
   float x;
   int tok;
 };
-
-__device__ __forceinline__ void atomic_put_u64(uint64_t* p, uint64_t v) {
-  uint64_t old = __hip_atomic_exchange(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  asm volatile("" ::"v"(old));
-}
 
 // ------------------------------------------------------------------ scan ---
 
@@ -2410,6 +2408,28 @@ __device__ __forceinline__ int resolve_accept_wave(const Args& a, int64_t b, int
   return len;
 }
 
+// Outputs of request b (len = -1: blocked).  With a cutoff the accepted
+// length is capped at cutoff[b] - 1 (at least 0) and a capped request's
+// bonus is its drafted token at the cap, which the target accepted
+// (cap_correct_len.py:44-52 and accept_sampling.py:151-157,185-186: the bonus is read
+// back from the chain's accepted slots).
+__device__ __forceinline__ void write_result(const Args& a, int64_t b, int len, int64_t tok) {
+  int trim = 0;
+  if (a.cutoff && len >= 0) {
+    const int cap = max(a.cutoff[b] - 1, 0);
+    if (cap < len) {
+      trim = len - cap;
+      len = cap;
+      const int64_t at = b * a.csb + static_cast<int64_t>(a.cfirst + cap) * a.csk;
+      tok = a.cand_i64 ? static_cast<const int64_t*>(a.cand)[at]
+                       : static_cast<int64_t>(static_cast<const int32_t*>(a.cand)[at]);
+    }
+  }
+  a.accept[b] = len;
+  a.bonus[b] = tok;
+  if (a.trim) a.trim[b] = trim;
+}
+
 // Final draw of request b when the target support at the accepted length and
 // the draft support (if a residual is needed) have at most 64 entries each
 // (one wave, one entry per lane): q of each target entry by matching indices,
@@ -2475,10 +2495,7 @@ __device__ __forceinline__ void resolve_wave(const Args& a, int64_t b, int len, 
   const int idx = static_cast<int>(key >> 32);
   const int first = hit ? __ffsll(static_cast<long long>(hit)) - 1 : 0;
   const int at = __shfl(idx, first, kWave);
-  if (lane == 0) {
-    a.accept[b] = len;
-    a.bonus[b] = (total > 0.f && hit) ? at : static_cast<int>(a.vocab - 1);
-  }
+  if (lane == 0) write_result(a, b, len, (total > 0.f && hit) ? at : a.vocab - 1);
 }
 
 // Wave 0 of the resolve kernel, after the accepted length and the draft
@@ -2508,8 +2525,7 @@ __device__ __forceinline__ bool resolve_finish(const Args& a, const WaveShared& 
                        (rejected && a.q_mode == 0 && (dr.flags & (kFlagOverflow | kFlagSkip)));
   if (blocked) {
     if (lane == 0) {
-      a.accept[b] = -1;
-      a.bonus[b] = -1;
+      write_result(a, b, -1, -1);
       if (a.status) atomicOr(a.status, kFlagOverflow);
     }
     return true;
@@ -2621,8 +2637,7 @@ __global__ __launch_bounds__(kT) void resolve_kernel(Args a) {
                        (rejected && a.q_mode == 0 && (dr.flags & (kFlagOverflow | kFlagSkip)));
   if (blocked) {
     if (tid == 0) {
-      a.accept[b] = -1;
-      a.bonus[b] = -1;
+      write_result(a, b, -1, -1);
       if (a.status) atomicOr(a.status, kFlagOverflow);
     }
     return;
@@ -2683,10 +2698,7 @@ __global__ __launch_bounds__(kT) void resolve_kernel(Args a) {
     const int hit = total > 0.f ? cdf_find(sh, static_cast<int>(a.vocab), u, [&](int i) { return val(i); }, total) : -1;
     tok = hit >= 0 ? hit : static_cast<int>(a.vocab - 1);
   }
-  if (tid == 0) {
-    a.accept[b] = len;
-    a.bonus[b] = tok;
-  }
+  if (tid == 0) write_result(a, b, len, tok);
 }
 
 inline uint64_t up256(uint64_t x) { return (x + 255) & ~uint64_t(255); }
@@ -2791,6 +2803,7 @@ extern "C" int ls_verify_sample(const ls_verify_sample_args* in, void* counters,
   a.d_min_ps = x.draft_min_ps;
   a.uni = x.uniforms; a.usb = x.uniform_stride_b; a.funi = x.final_uniforms;
   a.accept = x.accept_lens; a.bonus = x.bonus; a.p_cand_out = x.p_cand_out; a.status = x.status;
+  a.cutoff = x.cutoff_verify_lens; a.trim = x.cap_trim; a.cand_i64 = x.candidates_dtype == LS_I64;
   char* c = static_cast<char*>(counters);
   const int64_t rows = x.batch * x.width;
   a.cnt_t = reinterpret_cast<uint32_t*>(c);

@@ -122,9 +122,24 @@ def build_dflash_verify_target_probs(*, next_token_logits: torch.Tensor, samplin
     (no sparse top-k, or ``max_top_k >= V``) keeps ``top_k``; top-p applies
     when ``sampling_info.need_top_p_sampling``.  ``uniform_top_k_value`` only
     lets the reference skip a mask and changes no value."""
+    ks, ps, mk_bound = dflash_filter_params(sampling_info, int(next_token_logits.shape[-1]), max_top_k,
+                                            use_sparse_topk)
+    out = target_probs(logits=next_token_logits, temperatures=sampling_info.temperatures,
+                       rows_per_request=draft_token_num, top_ks=ks, top_ps=ps, max_top_k=mk_bound)
+    return out.view(bs, draft_token_num, -1)
+
+
+def dflash_filter_params(sampling_info: Any, vocab: int, max_top_k: Optional[int] = None,
+                         use_sparse_topk: bool = True):
+    """Per-request ``(top_ks, top_ps, max_top_k bound)`` of SPEC/dflash_utils.py:754-809.
+
+    top-k applies when ``need_top_k_sampling`` (k clamped to [1, V]); on the
+    sparse path the k of every row is further clamped to ``max_top_k`` (the
+    largest requested k when None, which costs a host read as in the
+    reference); top-p applies when ``need_top_p_sampling``.  None = filter off.
+    """
     need_top_k = bool(getattr(sampling_info, "need_top_k_sampling", True))
     need_top_p = bool(getattr(sampling_info, "need_top_p_sampling", False))
-    vocab = int(next_token_logits.shape[-1])
     ks = None
     mk_bound = None
     if need_top_k:
@@ -136,6 +151,4 @@ def build_dflash_verify_target_probs(*, next_token_logits: torch.Tensor, samplin
                 ks = ks.clamp(max=mk)
                 mk_bound = mk
     ps = sampling_info.top_ps if need_top_p else None
-    out = target_probs(logits=next_token_logits, temperatures=sampling_info.temperatures,
-                       rows_per_request=draft_token_num, top_ks=ks, top_ps=ps, max_top_k=mk_bound)
-    return out.view(bs, draft_token_num, -1)
+    return ks, ps, mk_bound

@@ -19,16 +19,35 @@ from typing import Dict, Iterable, List, Optional, Tuple
 
 def replacements() -> Dict[str, Dict[str, object]]:
     """module name -> {attribute: replacement}, for every hot-path call site."""
-    from . import dense, kvwindow, penalties, summary, verify
+    from . import accept, dense, kvwindow, penalties, summary, verify
 
     return {
         # greedy verify (SPEC/dspark_components/kernels/accept_greedy.py:22-60)
         "sglang.srt.speculative.dspark_components.kernels.accept_greedy": {"AcceptGreedy": verify.AcceptGreedy},
+        # stochastic acceptance (SPEC/dspark_components/kernels/accept_sampling.py:25-343) and its
+        # bindings of the chain sampler, SoftmaxTemp and the target distribution (:11-19)
+        "sglang.srt.speculative.dspark_components.kernels.accept_sampling": {
+            "AcceptSampling": accept.AcceptSampling, "accept_sampling": accept.accept_sampling,
+            "accept_sampling_single_q": accept.accept_sampling_single_q,
+            "chain_speculative_sampling_triton": accept.chain_speculative_sampling_triton,
+            "SoftmaxTemp": dense.SoftmaxTemp,
+            "build_dflash_verify_target_probs": dense.build_dflash_verify_target_probs},
+        # dense-q chain sampling (SPEC/reject_sampling.py:159-204)
+        "sglang.srt.speculative.reject_sampling": {
+            "chain_speculative_sampling_triton": accept.chain_speculative_sampling_triton},
+        # acceptance dispatch (SPEC/dspark_components/dspark_accept.py:20-159) and its bindings (:7-17)
+        "sglang.srt.speculative.dspark_components.dspark_accept": {
+            "accept_draft_tokens": accept.accept_draft_tokens,
+            "accept_scheduled_greedy_tokens": accept.accept_scheduled_greedy_tokens,
+            "AcceptGreedy": verify.AcceptGreedy, "AcceptSampling": accept.AcceptSampling,
+            "SoftmaxTemp": dense.SoftmaxTemp},
         # dense target distributions (SPEC/dspark_components/kernels/softmax_temp.py:17-175,
         # SPEC/dflash_utils.py:743-810)
         "sglang.srt.speculative.dspark_components.kernels.softmax_temp": {"SoftmaxTemp": dense.SoftmaxTemp},
         "sglang.srt.speculative.dflash_utils": {
-            "build_dflash_verify_target_probs": dense.build_dflash_verify_target_probs},
+            "build_dflash_verify_target_probs": dense.build_dflash_verify_target_probs,
+            # in-place verify logit adjustments (SPEC/dflash_utils.py:127-213)
+            "apply_dflash_verify_logits_adjustments": penalties.apply_dflash_verify_logits_adjustments},
         # split-engine two-phase rejection sampling (src/longspark/engine/sampling.py:19-57)
         "longspark.engine.sampling": {"decide_acceptance": verify.decide_acceptance,
                                       "finish_sampling": verify.finish_sampling},

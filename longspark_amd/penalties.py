@@ -116,3 +116,102 @@ def apply_token_bitmask_inplace(logits: torch.Tensor, bitmask: torch.Tensor) -> 
     if bitmask.shape[0] != logits.shape[0]:
         raise ValueError("batch size mismatch between logits and bitmask")
     adjust_logits_(logits, rows_per_request=1, vocab_mask=bitmask)
+
+
+def _request_rows(t: Optional[torch.Tensor], batch: int, vocab: int, what: str, name: str):
+    """fp32 ``[batch, vocab]`` with unit column stride (other float dtypes
+    convert exactly)."""
+    if t is None:
+        return None
+    if t.ndim == 1:
+        t = t.unsqueeze(0)
+    if t.shape != (batch, vocab):
+        raise ValueError(f"{what}: {name} must be [{batch}, {vocab}], got {tuple(t.shape)}")
+    if t.dtype != torch.float32:
+        t = t.float()
+    if t.stride(1) != 1:
+        t = t.contiguous()
+    return t
+
+
+def add_request_bias_(logits: torch.Tensor, *, rows_per_request: int, bias: Optional[torch.Tensor] = None,
+                      vocab_mask: Optional[torch.Tensor] = None, bias2: Optional[torch.Tensor] = None,
+                      separate: bool = False) -> None:
+    """In place on ``[B*rows_per_request, V]`` logits (``ls_add_request_bias``).
+
+    ``separate=False`` (SRT/speculative/dflash_utils.py:176-191): one combined
+    bias per request -- ``bias`` (0 when None), columns whose packed
+    ``vocab_mask`` bit is 0 set to -inf, plus ``bias2`` -- rounded to the
+    logits' dtype and added.  ``separate=True`` (:193-213): ``bias`` then
+    ``bias2`` added one after the other, each rounded to the logits' dtype.
+    """
+    what = "add_request_bias_"
+    dev = _lib.require_cuda(logits, bias, vocab_mask, bias2, what=what)
+    if logits.ndim != 2 or logits.stride(1) != 1:
+        raise ValueError(f"{what}: logits must be [rows, V] with unit column stride")
+    rows, vocab = logits.shape
+    if rows_per_request <= 0 or rows % rows_per_request != 0:
+        raise ValueError(f"{what}: {rows} rows are not a multiple of {rows_per_request}")
+    batch = rows // rows_per_request
+    bias = _request_rows(bias, batch, vocab, what, "bias")
+    bias2 = _request_rows(bias2, batch, vocab, what, "bias2")
+    if vocab_mask is not None:
+        if separate:
+            raise ValueError(f"{what}: the mask belongs to the combined form")
+        if vocab_mask.dtype != torch.int32 or vocab_mask.ndim != 2 or vocab_mask.shape[0] != batch or \
+                vocab_mask.stride(1) != 1 or vocab_mask.shape[1] > (vocab + 31) // 32:
+            raise ValueError(f"{what}: vocab_mask must be int32 [{batch}, <= {(vocab + 31) // 32}]")
+    _lib.call("ls_add_request_bias", logits.data_ptr(), _lib.dtype_code(logits), logits.stride(0), rows, vocab,
+              rows_per_request, _lib.ptr(bias), bias.stride(0) if bias is not None else 0,
+              _lib.ptr(vocab_mask), vocab_mask.stride(0) if vocab_mask is not None else 0,
+              vocab_mask.shape[1] if vocab_mask is not None else 0,
+              _lib.ptr(bias2), bias2.stride(0) if bias2 is not None else 0, int(bool(separate)),
+              _lib.stream_of(dev))
+
+
+def _custom_logit_processor(logits, sampling_info, draft_token_num):
+    try:  # the caller's own processors live in the serving stack
+        from sglang.srt.layers.sampler import apply_custom_logit_processor
+    except ImportError as e:
+        raise RuntimeError("custom logit processors need the serving stack's apply_custom_logit_processor") from e
+    apply_custom_logit_processor(logits, sampling_info, num_tokens_in_batch=draft_token_num)
+
+
+def apply_dflash_verify_logits_adjustments(*, next_token_logits: torch.Tensor, sampling_info,
+                                           draft_token_num: int) -> None:
+    """Drop-in for SRT/speculative/dflash_utils.py:127-213, in place.
+
+    The dense path (live penalisers without ``acc_linear_penalties``, or a
+    grammar mask) builds the request bias exactly as the reference does --
+    ``sampling_info.apply_logits_bias`` on a zero fp32 ``[B, V]`` tensor, so
+    scaling penalties act on zeros -- and the gfx950 kernel adds it to all
+    ``draft_token_num`` rows of each request in the logits' dtype.  Otherwise
+    ``acc_linear_penalties`` and ``logit_bias`` are added one after the other
+    by the same kernel.
+    """
+    if sampling_info is None:
+        return
+    if next_token_logits.ndim != 2:
+        raise ValueError(f"next_token_logits must be 2D, got shape={tuple(next_token_logits.shape)}.")
+    if draft_token_num <= 0:
+        raise ValueError(f"draft_token_num must be positive, got {draft_token_num}.")
+    bs = len(sampling_info)
+    if next_token_logits.shape[0] != bs * draft_token_num:
+        raise ValueError("next_token_logits row count mismatch for DFlash verify adjustments. "
+                         f"Expected {bs * draft_token_num}, got {next_token_logits.shape[0]}.")
+    if getattr(sampling_info, "has_custom_logit_processor", False):
+        _custom_logit_processor(next_token_logits, sampling_info, draft_token_num)
+    acc = getattr(sampling_info, "acc_linear_penalties", None)
+    penalizer = getattr(sampling_info, "penalizer_orchestrator", None)
+    vocab_mask = getattr(sampling_info, "vocab_mask", None)
+    logit_bias = getattr(sampling_info, "logit_bias", None)
+    vocab = next_token_logits.shape[1]
+    if (penalizer is not None and penalizer.is_required and acc is None) or vocab_mask is not None:
+        linear_penalty = torch.zeros((bs, vocab), dtype=torch.float32, device=next_token_logits.device)
+        sampling_info.apply_logits_bias(linear_penalty)
+        add_request_bias_(next_token_logits, rows_per_request=draft_token_num, bias=linear_penalty)
+        return
+    if acc is None and logit_bias is None:
+        return
+    add_request_bias_(next_token_logits, rows_per_request=draft_token_num, bias=acc, bias2=logit_bias,
+                      separate=True)

@@ -265,7 +265,8 @@ def verify_sample(*, logits: torch.Tensor, candidates: torch.Tensor, width: int,
                   draft_temperatures=None, draft_top_ks=None, draft_top_ps=None, draft_min_ps=None,
                   penalties=None, vocab_mask: Optional[torch.Tensor] = None, mask_per_request: bool = False,
                   cand_first_col: int = 1, return_p_cand: bool = False, check: bool = False,
-                  timing_events=None, scan_hint: int = 0):
+                  timing_events=None, scan_hint: int = 0, cutoff_verify_lens: Optional[torch.Tensor] = None,
+                  return_cap_trim: bool = False):
     """Fused stochastic verify of a drafted block (one call, three kernels).
 
     Target: ``logits`` ``[B*width, V]`` (bf16/fp16/fp32) with penalties
@@ -277,8 +278,11 @@ def verify_sample(*, logits: torch.Tensor, candidates: torch.Tensor, width: int,
     the ``draft_*`` parameters; pure temperature when they are None), or dense
     ``draft_probs [B, width-1, V]`` fp32 (q read directly).
     Randomness: ``uniforms [B, width-1]`` and ``final_uniforms [B]`` fp32.
-    Returns ``(accept_lens i32[B], bonus i64[B])`` (plus the per-drafted-token
-    target probabilities ``[B, width-1]`` with ``return_p_cand``).  With
+    ``cutoff_verify_lens`` ``[B]``: the accepted length is capped at
+    ``cutoff - 1`` (a capped request's bonus is its drafted token at the cap).
+    Returns ``(accept_lens i32[B], bonus i64[B])``, then ``cap_trim i32[B]``
+    with ``return_cap_trim`` and the per-drafted-token target probabilities
+    ``[B, width-1]`` with ``return_p_cand``.  With
     ``check`` the call synchronises and raises if a request could not be
     resolved (such requests get -1 in both outputs).  ``timing_events``: an
     optional ctypes array of 4 hipEvent_t recorded around the kernels.
@@ -291,7 +295,7 @@ def verify_sample(*, logits: torch.Tensor, candidates: torch.Tensor, width: int,
     logits = _rows_view(logits, width, what)
     draft = draft_probs if draft_probs is not None else draft_logits
     dev = _lib.require_cuda(logits, candidates, uniforms, final_uniforms, draft, draft_token_probs, vocab_mask,
-                            what=what)
+                            cutoff_verify_lens, what=what)
     if candidates.ndim != 2 or candidates.dtype not in (torch.int32, torch.int64):
         raise ValueError(f"{what}: candidates must be [B, C] int32/int64")
     batch = candidates.shape[0]
@@ -334,8 +338,13 @@ def verify_sample(*, logits: torch.Tensor, candidates: torch.Tensor, width: int,
         if vocab_mask.dtype != torch.int32 or vocab_mask.shape != (rows_m, words) or vocab_mask.stride(1) != 1:
             raise ValueError(f"{what}: vocab_mask must be [{rows_m}, {words}] int32")
     mk = 0 if max_top_k is None else int(max_top_k)
+    if cutoff_verify_lens is not None:
+        if cutoff_verify_lens.shape != (batch,):
+            raise ValueError(f"{what}: cutoff_verify_lens must be [batch]")
+        cutoff_verify_lens = cutoff_verify_lens.to(torch.int32).contiguous()
 
     accept = torch.empty(batch, dtype=torch.int32, device=dev)
+    trim = torch.empty(batch, dtype=torch.int32, device=dev) if return_cap_trim else None  # written per request
     bonus = torch.empty(batch, dtype=torch.int64, device=dev)
     p_cand = torch.empty(batch, g, dtype=torch.float32, device=dev) if return_p_cand else None
     status = torch.empty(1, dtype=torch.int32, device=dev)  # cleared by the call's first kernel
@@ -369,6 +378,7 @@ def verify_sample(*, logits: torch.Tensor, candidates: torch.Tensor, width: int,
     if scan_hint not in (0, 1, 2):
         raise ValueError(f"{what}: scan_hint must be 0, 1 or 2")
     a.scan_hint = scan_hint
+    a.cutoff_verify_lens, a.cap_trim = _lib.ptr(cutoff_verify_lens), _lib.ptr(trim)
     if timing_events is not None:
         a.timing_events = _lib.ctypes.cast(timing_events, _lib.ctypes.c_void_p)
     cnt, scr = _lib.workspaces.get(*_lib.workspace_sizes("ls_verify_sample_workspace", batch, width, vocab, mk), dev)
@@ -378,9 +388,12 @@ def verify_sample(*, logits: torch.Tensor, candidates: torch.Tensor, width: int,
         torch.cuda.synchronize(dev)
         if int(status.item()) != 0:
             raise RuntimeError(f"{what}: a request's sampling support exceeded the kernel capacity")
+    out = (accept, bonus)
+    if return_cap_trim:
+        out += (trim,)
     if return_p_cand:
-        return accept, bonus, p_cand
-    return accept, bonus
+        out += (p_cand,)
+    return out
 
 
 def ctypes_byref(struct):

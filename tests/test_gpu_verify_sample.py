@@ -158,7 +158,6 @@ def test_dense_draft_probs(dev):
     x = c["logits"].float()
     probs = ov.target_probs(x, temperatures=p.temperatures, top_ks=p.top_ks, top_ps=p.top_ps, min_ps=p.min_ps,
                             rows_per_request=8).view(4, 8, 30000)
-    _, _, _ = None, None, None
     preds, aidx, anum = ov.chain_speculative_sampling(
         candidates=c["candidates"].long(), uniform_samples=c["uniforms"], uniform_final=c["final_uniforms"],
         target_probs_3d=probs, draft_probs_3d=q)

@@ -187,6 +187,56 @@ def test_chain_sampling_matches_single_q_when_q_is_dense_softmax():
     assert (chain_bonus == bonus).float().mean() > 0.9
 
 
+def test_chain_sampling_hand_cases():
+    """reject_sampling.py:5-156 by hand: acceptance u*q < p on the drafted
+    token's row, residual max(p - q, 0) (not normalised) with the first index
+    whose running sum exceeds u_final * total, all-accepted draws from the
+    last target row, a zero residual gives vocab-1, and the predicts /
+    accept_index layout over retrive_index = arange(B*K)."""
+    p = torch.tensor([[[0.3, 0.3, 0.4, 0.0], [0.1, 0.2, 0.3, 0.4], [0.1, 0.2, 0.3, 0.4]],
+                      [[0.3, 0.3, 0.4, 0.0], [0.1, 0.2, 0.3, 0.4], [0.1, 0.2, 0.3, 0.4]],
+                      [[0.5, 0.5, 0.0, 0.0], [0.1, 0.2, 0.3, 0.4], [0.1, 0.2, 0.3, 0.4]],
+                      [[0.25, 0.25, 0.25, 0.25], [0.1, 0.2, 0.3, 0.4], [0.1, 0.2, 0.3, 0.4]]])
+    q = torch.tensor([[[0.1, 0.5, 0.1, 0.3], [0.1, 0.2, 0.3, 0.4]],
+                      [[0.1, 0.5, 0.1, 0.3], [0.1, 0.2, 0.3, 0.4]],
+                      [[0.5, 0.5, 0.0, 0.0], [0.1, 0.2, 0.3, 0.4]],
+                      [[0.25, 0.25, 0.25, 0.25], [0.1, 0.2, 0.3, 0.4]]])
+    cand = torch.tensor([[9, 1, 3], [9, 1, 3], [9, 3, 0], [9, 2, 3]])
+    u = torch.tensor([[0.8, 0.0], [0.8, 0.0], [0.5, 0.5], [0.9, 0.9]])
+    uf = torch.tensor([0.5, 0.3, 0.7, 0.35])
+    preds, aidx, anum = ov.chain_speculative_sampling(candidates=cand, uniform_samples=u, uniform_final=uf,
+                                                      target_probs_3d=p, draft_probs_3d=q)
+    # b0: 0.8*0.5 >= 0.3 rejects; residual [0.2, 0, 0.3, 0], 0.5*0.5 = 0.25 -> index 2
+    # b1: same residual, 0.3*0.5 = 0.15 -> index 0
+    # b2: token 3 has p = 0: rejected; residual all zero -> vocab-1
+    # b3: q = p on both rows: both accepted (u*q < q); bonus from p[2] at 0.35 -> index 2
+    assert anum.tolist() == [0, 0, 0, 2]
+    bonus = preds[aidx[torch.arange(4), anum.long()].long()].tolist()
+    assert bonus == [2, 0, 3, 2]
+    assert aidx[3].tolist() == [9, 10, 11] and preds[9:12].tolist() == [2, 3, 2]
+
+
+@pytest.mark.slow
+def test_chain_sampling_is_lossless():
+    """With one drafted token drawn from the dense q row, the first emitted
+    token (the accepted draft, or the residual draw) follows p (chi-square,
+    20k trials, V=6)."""
+    g = torch.Generator().manual_seed(2)
+    v, n = 6, 20_000
+    p = torch.softmax(torch.tensor([1.0, 0.2, -0.5, 0.8, 0.0, -1.0]), 0)
+    q = torch.softmax(torch.tensor([0.1, 0.9, 0.3, -0.2, 0.5, 0.0]), 0)
+    drafted = torch.multinomial(q, n, replacement=True, generator=g)
+    cand = torch.stack([torch.zeros(n, dtype=torch.long), drafted], 1)
+    preds, aidx, anum = ov.chain_speculative_sampling(
+        candidates=cand, uniform_samples=torch.rand(n, 1, generator=g), uniform_final=torch.rand(n, generator=g),
+        target_probs_3d=p.expand(n, 2, v), draft_probs_3d=q.expand(n, 1, v))
+    first = preds[aidx[:, 0].long()].long()
+    counts = torch.bincount(first, minlength=v).double()
+    expected = p.double() * n
+    chi2 = float(((counts - expected) ** 2 / expected).sum())
+    assert chi2 < 25.0, (chi2, counts, expected)  # 5 dof, p ~ 1e-4
+
+
 def test_finalize_outputs_hand_case():
     cand = torch.tensor([[5, 11, 12, 13], [7, 21, 22, 23]])
     out, committed, nxt = ov.finalize_verify_outputs(cand, torch.tensor([1, 3], dtype=torch.int32),

@@ -4,12 +4,13 @@ reference's own patches do (src/longspark/patches/__init__.py:15-33)."""
 import sys
 import types
 
-from longspark_amd import patches, summary, kvwindow, verify
+from longspark_amd import accept, patches, summary, kvwindow, verify
 
 
 def test_install_replaces_attributes_of_importable_modules(monkeypatch):
     names = ["sglang.srt.speculative.global16_raw256_incremental", "longspark.engine.draft",
-             "longspark.engine.sampling"]
+             "longspark.engine.sampling", "sglang.srt.speculative.reject_sampling",
+             "sglang.srt.speculative.dspark_components.dspark_accept"]
     for n in names:
         parts = n.split(".")
         for i in range(1, len(parts) + 1):
@@ -23,6 +24,9 @@ def test_install_replaces_attributes_of_importable_modules(monkeypatch):
     assert inc.merge_accepted_positions_ is summary.merge_accepted_positions_
     assert sys.modules[names[1]].ring_page_table is kvwindow.ring_page_table
     assert sys.modules[names[2]].decide_acceptance is verify.decide_acceptance
+    assert sys.modules[names[3]].chain_speculative_sampling_triton is accept.chain_speculative_sampling_triton
+    assert sys.modules[names[4]].accept_draft_tokens is accept.accept_draft_tokens
+    assert sys.modules[names[4]].AcceptSampling is accept.AcceptSampling
 
 
 def test_every_replacement_target_is_listed_once():

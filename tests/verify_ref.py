@@ -73,7 +73,31 @@ def _support_boundary_near(c, probs_row_logits, temperature, top_k, top_p, min_p
     return near
 
 
-def classify(c, lens_k, bonus_k, lens_r, bonus_r, probs_r, p_cand_k=None):
+def cdf_tie(vals, u, tok_a, tok_b) -> bool:
+    """Two inverse-CDF draws from ``vals`` (first index whose running sum
+    exceeds ``u * total``) that differ only by rounding: the running sum at the
+    earlier of the two tokens lies within TIE * total of ``u * total``."""
+    vals = vals.double()
+    cdf = torch.cumsum(vals, 0)
+    total = float(cdf[-1])
+    t = min(int(tok_a), int(tok_b))
+    if total <= 0.0 or t < 0 or t >= vals.numel():
+        return False
+    return abs(float(cdf[t]) - float(u) * total) <= TIE * total
+
+
+def bonus_row(probs_row, q_row, rejected: bool, single_q: bool):
+    """The distribution the bonus is drawn from: p, or max(p - q, 0) after a
+    rejection (single-q acceptance falls back to p below 1e-8 of mass)."""
+    if not rejected:
+        return probs_row.double()
+    r = (probs_row.double() - q_row.double()).clamp_min(0.0)
+    if single_q and float(r.sum()) <= ov.RESIDUAL_MASS_EPS:
+        return probs_row.double()
+    return r
+
+
+def classify(c, lens_k, bonus_k, lens_r, bonus_r, probs_r, p_cand_k=None, draft_params=True):
     """Returns (mismatched_requests, exempt_requests, messages)."""
     bsz, width = c["candidates"].shape
     g = width - 1
@@ -108,17 +132,17 @@ def classify(c, lens_k, bonus_k, lens_r, bonus_r, probs_r, p_cand_k=None):
             msgs.append(f"b={b}: p_cand differs: kernel {p_cand_k[b].tolist()} ref "
                         f"{probs_r[b, torch.arange(g), cand[b, 1:]].tolist()}")
             continue
-        if not same and not reasons:
-            # inverse-CDF tie of the final draw
-            row = probs_r[b, int(lens_r[b])].double()
-            vals = row
-            if int(lens_r[b]) < g:
-                # the residual distribution is not materialised by the oracle's
-                # public API; recompute it here for the margin check
-                pass
-            cdf = torch.cumsum(vals, 0)
-            thr = float(c["final_uniforms"][b]) * float(cdf[-1])
-            if bool(((cdf - thr).abs() <= TIE * float(cdf[-1])).any()):
+        if not same and not reasons and int(lens_k[b]) == int(lens_r[b]):
+            # inverse-CDF tie of the final draw, on the row the bonus is drawn from
+            lr = int(lens_r[b])
+            q_row = None
+            if lr < g:
+                kw = dict(top_ks=p.top_ks, top_ps=p.top_ps, min_ps=p.min_ps) if draft_params else {}
+                q_row = ov.draft_q_rows(c["draft_logits"][b:b + 1], torch.tensor([lr]),
+                                        temperatures=p.temperatures[b:b + 1],
+                                        **{k: v[b:b + 1] for k, v in kw.items()})[0]
+            vals = bonus_row(probs_r[b, lr], q_row, lr < g, single_q=True)
+            if cdf_tie(vals, float(c["final_uniforms"][b]), int(bonus_k[b]), int(bonus_r[b])):
                 reasons.append("cdf tie")
         if reasons:
             exempt.append(b)
