@@ -5,10 +5,12 @@
 // One workgroup of 1024 threads per row.  The first pass reads the row once
 // and keeps, per thread, an online maximum and the sum of exponentials
 // rescaled whenever the maximum rises; the per-thread pairs are combined
-// across the workgroup.  The second pass reads the row again (it is still
-// in the last-level cache for the rows in flight) and writes the
-// probabilities as fp32.  Rows 16-byte aligned (start and stride) move
-// as 16-byte vectors; others element by element.
+// across the workgroup.  The second pass reads the row again in 4-element
+// units and writes the probabilities as fp32, one whole 16-byte vector per
+// lane, so that every store instruction covers whole cache lines (two 16-byte
+// stores 32 bytes apart per lane half-fill each line they touch and cost 1.5x
+// the write traffic).  Rows 16-byte aligned (start and stride) move as
+// vectors; others element by element.
 #include "rowscan.h"
 
 namespace ls {
@@ -21,6 +23,26 @@ constexpr int kSTU = 4;     // vectors per thread in flight
 // reference's exp(l / T - max(l / T)) / sum up to the rounding of its fp32
 // quotient (a relative difference of about |l - l_max| / T * 2^-24 in p).
 // The per-thread sums are kept in fp64 (one fp32 partial per vector).
+
+// Four consecutive elements as fp32: one 8-byte load for 16-bit types, one
+// 16-byte load for fp32 (p: 4-element aligned).  The second pass reads its
+// input in these units so that each lane writes one 16-byte output vector and
+// a wavefront's store covers 1 KiB contiguously (whole cache lines).
+template <typename Tag>
+__device__ __forceinline__ void load4_stream(const typename Tag::storage* p, float* x) {
+  if constexpr (sizeof(typename Tag::storage) == 2) {
+    const uint32_t* q = reinterpret_cast<const uint32_t*>(p);
+    const uint32_t a = __builtin_nontemporal_load(q), b = __builtin_nontemporal_load(q + 1);
+    uint4 v;
+    v.x = a; v.y = b; v.z = 0u; v.w = 0u;
+    float t[8];
+    unpack16<Tag>(v, t);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) x[e] = t[e];
+  } else {
+    unpack16<Tag>(load16_stream(p), x);
+  }
+}
 
 template <typename Tag, bool kVec>
 __global__ __launch_bounds__(kST) void softmax_temp_kernel(const typename Tag::storage* __restrict__ logits,
@@ -105,33 +127,31 @@ __global__ __launch_bounds__(kST) void softmax_temp_kernel(const typename Tag::s
     if (wm[w] != -INFINITY) z += wsum[w] * static_cast<double>(__builtin_amdgcn_exp2f((wm[w] - rm) * c2));
   const float inv = static_cast<float>(1.0 / z);
 
-  // pass 2: p = exp2((l - max) * c2) / sum
+  // pass 2: p = exp2((l - max) * c2) / sum, in units of 4 elements
+  int64_t tail = 0;
   if constexpr (kVec) {
-    for (int64_t v0 = tid; v0 < nvec; v0 += kSTU * kST) {
-      uint4 buf[kSTU];
+    constexpr int kU = sizeof(S) == 2 ? 2 * kSTU : kSTU;  // 8-byte loads: twice as many in flight
+    const int64_t n4 = vocab / 4;
+    for (int64_t v0 = tid; v0 < n4; v0 += kU * kST) {
+      float x[kU][4];
 #pragma unroll
-      for (int u = 0; u < kSTU; ++u) buf[u] = load16_stream(vp + min<int64_t>(v0 + u * kST, nvec - 1));
+      for (int u = 0; u < kU; ++u) load4_stream<Tag>(rp + min<int64_t>(v0 + u * kST, n4 - 1) * 4, x[u]);
 #pragma unroll
-      for (int u = 0; u < kSTU; ++u) {
+      for (int u = 0; u < kU; ++u) {
         const int64_t v = v0 + u * kST;
-        if (v < nvec) {
-          float x[P];
-          unpack16<Tag>(buf[u], x);
-          float4* o4 = reinterpret_cast<float4*>(op + v * P);
-#pragma unroll
-          for (int h = 0; h < P / 4; ++h) {
-            float4 y;
-            y.x = __builtin_amdgcn_exp2f((x[4 * h + 0] - rm) * c2) * inv;
-            y.y = __builtin_amdgcn_exp2f((x[4 * h + 1] - rm) * c2) * inv;
-            y.z = __builtin_amdgcn_exp2f((x[4 * h + 2] - rm) * c2) * inv;
-            y.w = __builtin_amdgcn_exp2f((x[4 * h + 3] - rm) * c2) * inv;
-            store16_stream(o4 + h, y);
-          }
+        if (v < n4) {
+          float4 y;
+          y.x = __builtin_amdgcn_exp2f((x[u][0] - rm) * c2) * inv;
+          y.y = __builtin_amdgcn_exp2f((x[u][1] - rm) * c2) * inv;
+          y.z = __builtin_amdgcn_exp2f((x[u][2] - rm) * c2) * inv;
+          y.w = __builtin_amdgcn_exp2f((x[u][3] - rm) * c2) * inv;
+          store16_stream(op + v * 4, y);
         }
       }
     }
+    tail = n4 * 4;
   }
-  for (int64_t e = nvec * P + tid; e < vocab; e += kST)
+  for (int64_t e = tail + tid; e < vocab; e += kST)
     op[e] = __builtin_amdgcn_exp2f((to_f32<S>(rp[e]) - rm) * c2) * inv;
 }
 
