@@ -533,6 +533,45 @@ class ChainSampling:
                 "sample": f"{b} requests, oracle torch-CPU chain sampling, median of {n} runs"}
 
 
+class SampleStep:
+    """sample_step_tokens_with_q: the drafter's per-step exponential race with
+    the sampled q over fp32 logits [128, 151,936] and fp32 Exp(1) noise of the
+    same shape (one proposal step of a batch of 128)."""
+
+    name = "sample_step"
+    metric = "proposal-step sampling GB/s (algorithmic bytes) at 128x151936 fp32 logits + fp32 noise"
+    unit = "GB/s"
+    dtype = "f32"
+
+    def __init__(self, dev, batch=128, vocab=V):
+        g = torch.Generator(device=dev).manual_seed(84)
+        self.batch, self.vocab = batch, vocab
+        self.logits = 3.0 * torch.randn(batch, vocab, generator=g, device=dev)
+        self.temps = torch.linspace(0.5, 1.5, batch, device=dev)
+        self.noise = torch.empty(batch, vocab, device=dev).exponential_(1, generator=g)
+        self.bytes = batch * vocab * 8     # every logit and noise value read once
+        self.units = self.bytes / 1e9
+        self.kernel = "sample_step_kernel"
+
+    def step(self):
+        from longspark_amd import sample
+        return sample.sample_step_tokens_with_q(step_logits=self.logits, temperatures=self.temps,
+                                                exp_noise=self.noise)
+
+    def config(self):
+        return {"workload": f"proposal step B={self.batch} V={self.vocab} fp32 logits + fp32 noise",
+                "batch": self.batch, "vocab": self.vocab}
+
+    def cpu_baseline(self, threads):
+        from oracle import verify as ov
+        torch.set_num_threads(threads)
+        b = 16
+        x, t, n = self.logits[:b].cpu(), self.temps[:b].cpu(), self.noise[:b].cpu()
+        med, k = time_cpu(lambda: ov.sample_step_tokens_with_q(x, t, n))
+        return {"value": b * self.vocab * 8 / med / 1e9, "threads": threads,
+                "sample": f"{b} rows, oracle torch-CPU exponential race, median of {k} runs"}
+
+
 class _BatchInfo(SimpleNamespace):
     """The sampling-info fields the verify logit adjustments read (one entry per request)."""
 
@@ -591,7 +630,7 @@ class AdjustLogits:
 
 
 WORKLOADS = {w.name: w for w in (GreedyVerify, StochasticVerify, WindowGather, SummaryUpdate, SoftmaxTempWorkload,
-                                  TargetProbsWorkload, ChainSampling, AdjustLogits, HbmCopy)}
+                                  TargetProbsWorkload, ChainSampling, AdjustLogits, SampleStep, HbmCopy)}
 DEFAULT_WORKLOAD = "verify_sample"
 
 

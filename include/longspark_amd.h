@@ -421,6 +421,27 @@ LS_API int ls_finalize_verify_outputs(const void* candidates, int32_t candidates
                                       int32_t* committed, void* next_lengths, void* stream);
 
 /* ---------------------------------------------------------------------------
+ * Drafter proposal step: replaces
+ * SRT/speculative/dspark_components/kernels/sample_step_tokens_with_q.py:72-382
+ * (sample_step_tokens_with_q: the exponential race with the sampled q).
+ * logits [rows, vocab] (fp32/bf16/fp16, unit column stride), temperatures
+ * [rows] fp32, exp_noise [rows, vocab] fp32 (E ~ Exp(1), row stride
+ * noise_row_stride).  Per row: s = l / T for finite l (else -inf),
+ * p = softmax(s); next_tokens[r] = argmax p / E (lowest index on ties),
+ * sampled_q[r] = p at that token.  A row with a NaN or +inf logit, an invalid
+ * l / T, noise outside (0, inf) at a finite entry, T outside (0, inf), or no
+ * finite entry gets token 0 and q = NaN and sets *status to 1 (status may be
+ * NULL; the caller clears it).  Workspace sizes from ls_sample_step_workspace;
+ * the counters must be zero on entry and are zero again when the call's work
+ * ends.
+ * ------------------------------------------------------------------------- */
+LS_API int ls_sample_step_workspace(int64_t rows, int64_t vocab, uint64_t* counter_bytes, uint64_t* scratch_bytes);
+LS_API int ls_sample_step(const void* logits, int32_t logits_dtype, int64_t logits_row_stride, int64_t rows,
+                          int64_t vocab, const float* temperatures, const float* exp_noise, int64_t noise_row_stride,
+                          int64_t* next_tokens, float* sampled_q, int32_t* status, void* counters,
+                          uint64_t counter_bytes, void* scratch, uint64_t scratch_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
  * Recent-window page tables, window gather and ring append.
  * ------------------------------------------------------------------------- */
 

@@ -19,7 +19,7 @@ from typing import Dict, Iterable, List, Optional, Tuple
 
 def replacements() -> Dict[str, Dict[str, object]]:
     """module name -> {attribute: replacement}, for every hot-path call site."""
-    from . import accept, dense, kvwindow, penalties, summary, verify
+    from . import accept, dense, kvwindow, penalties, sample, summary, verify
 
     return {
         # greedy verify (SPEC/dspark_components/kernels/accept_greedy.py:22-60)
@@ -48,6 +48,11 @@ def replacements() -> Dict[str, Dict[str, object]]:
             "build_dflash_verify_target_probs": dense.build_dflash_verify_target_probs,
             # in-place verify logit adjustments (SPEC/dflash_utils.py:127-213)
             "apply_dflash_verify_logits_adjustments": penalties.apply_dflash_verify_logits_adjustments},
+        # drafter proposal step (SPEC/dspark_components/kernels/sample_step_tokens_with_q.py:40-382;
+        # its callers import it at call time)
+        "sglang.srt.speculative.dspark_components.kernels.sample_step_tokens_with_q": {
+            "sample_step_tokens_with_q": sample.sample_step_tokens_with_q,
+            "create_sample_step_workspace": sample.create_sample_step_workspace},
         # split-engine two-phase rejection sampling (src/longspark/engine/sampling.py:19-57)
         "longspark.engine.sampling": {"decide_acceptance": verify.decide_acceptance,
                                       "finish_sampling": verify.finish_sampling},

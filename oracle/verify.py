@@ -488,3 +488,45 @@ def out_tokens(candidates, accept_lens, bonus):
     out[:, :-1] = candidates[:, 1:].long()
     out.scatter_(1, accept_lens.long()[:, None], bonus.long()[:, None])
     return out
+
+
+# --------------------------------------------------------------------------
+# drafter proposal step: exponential race with the sampled q
+# --------------------------------------------------------------------------
+
+def sample_step_tokens_with_q(step_logits, temperatures, exp_noise, *, compute_dtype=torch.float32):
+    """SPEC/dspark_components/kernels/sample_step_tokens_with_q.py:72-187 over whole rows.
+
+    The reference reduces 1024-element tiles and rescales each tile by
+    exp(m_t - m); over a whole row that is ``p = softmax(s)`` with
+    ``s = l / T`` for finite ``l`` (-inf otherwise), key ``p / E`` (-1 where
+    the noise is not in (0, inf)), token = first index of the largest key,
+    q = p at the token.  Invalid rows (:97-106, :170-176) give token 0 and
+    q = NaN.  Returns ``(tokens i64[N], q f32[N], valid bool[N])``.
+    """
+    x = step_logits.float()
+    t = temperatures.float().reshape(-1, 1)
+    noise = exp_noise.to(compute_dtype)
+    finite = torch.isfinite(x)
+    scaled = torch.where(finite, x / t, torch.full_like(x, float("-inf")))
+    logits_valid = ~torch.isnan(x) & (x != float("inf"))
+    scaled_valid = ~torch.isnan(scaled) & (scaled != float("inf"))
+    noise_valid = (noise > 0) & torch.isfinite(noise)
+    lane_valid = logits_valid & scaled_valid & torch.where(torch.isfinite(scaled), noise_valid,
+                                                           torch.ones_like(noise_valid))
+    temp_valid = (t.reshape(-1) > 0) & torch.isfinite(t.reshape(-1))
+    s = scaled.to(compute_dtype)
+    m = s.max(dim=-1).values
+    m_fin = torch.isfinite(m)
+    safe = torch.where(m_fin, m, torch.zeros_like(m))
+    e = torch.where(finite & m_fin[:, None], torch.exp(s - safe[:, None]), torch.zeros_like(s))
+    z = e.sum(dim=-1)
+    keys = torch.where(m_fin[:, None] & noise_valid, e / noise, torch.full_like(e, -1.0))
+    best = keys.max(dim=-1).values
+    idx = torch.argmax((keys == best[:, None]).to(torch.int8), dim=-1)  # first index of the maximum
+    q = e.gather(1, idx[:, None]).squeeze(1) / z
+    valid = temp_valid & lane_valid.all(dim=-1) & m_fin & torch.isfinite(z) & (z > 0)
+    tokens = torch.where(valid, idx, torch.zeros_like(idx)).to(torch.int64)
+    q = torch.where(valid, q, torch.full_like(q, float("nan"))).float()
+    return tokens, q, valid
+

@@ -244,3 +244,73 @@ def test_finalize_outputs_hand_case():
     # request 0 accepts one draft (11), bonus at column 1; request 1 accepts all three
     assert out.tolist() == [[11, 99, 13, 0], [21, 22, 23, 98]]
     assert committed.tolist() == [2, 4] and nxt.tolist() == [102, 204]
+
+
+# ---------------------------------------------------------------- proposal step
+
+def test_exponential_race_samples_p():
+    """argmax_v p_v / E_v with E ~ Exp(1) draws v with probability p_v
+    (chi-square, 60k rows, V=6), and q is p at the drawn token."""
+    g = torch.Generator().manual_seed(5)
+    n, v = 60_000, 6
+    logits = torch.tensor([1.0, 0.2, -0.5, 0.8, 0.0, -1.0]).expand(n, v)
+    t = torch.full((n,), 0.9)
+    noise = torch.empty(n, v).exponential_(1, generator=g)
+    tokens, q, valid = ov.sample_step_tokens_with_q(logits, t, noise)
+    p = torch.softmax(logits[0].double() / 0.9, 0)
+    assert bool(valid.all())
+    counts = torch.bincount(tokens, minlength=v).double()
+    chi2 = float(((counts - p * n) ** 2 / (p * n)).sum())
+    assert chi2 < 25.0, (chi2, counts, p * n)
+    assert torch.allclose(q.double(), p[tokens], rtol=1e-6)
+
+
+def test_sample_step_tile_combine_equals_whole_row():
+    """The reference's tile form (sample_step_tokens_with_q.py:72-187: tile max
+    m_t, sums and keys relative to m_t, combined with exp(m_t - m)) equals the
+    whole-row softmax form in fp64."""
+    g = torch.Generator().manual_seed(6)
+    rows, vocab, tile = 5, 3000, 1024
+    x = 3 * torch.randn(rows, vocab, generator=g, dtype=torch.float64)
+    x[:, 1500:2700] = float("-inf")       # a tile with no finite entry, a partly masked tile
+    t = torch.tensor([0.5, 0.8, 1.0, 1.3, 2.0], dtype=torch.float64)
+    noise = torch.empty(rows, vocab, dtype=torch.float64).exponential_(1, generator=g)
+    tok_ref, q_ref, _ = ov.sample_step_tokens_with_q(x, t, noise, compute_dtype=torch.float64)
+    s = x / t[:, None]
+    for r in range(rows):
+        tm, ts, tk, ti, tn = [], [], [], [], []
+        for c0 in range(0, vocab, tile):
+            seg, nz = s[r, c0:c0 + tile], noise[r, c0:c0 + tile]
+            m = seg.max()
+            e = torch.exp(seg - m) if torch.isfinite(m) else torch.zeros_like(seg)
+            keys = torch.where(torch.isfinite(m) & torch.ones_like(seg, dtype=torch.bool), e / nz,
+                               torch.full_like(seg, -1.0))
+            k = int(torch.argmax(keys))
+            tm.append(m), ts.append(e.sum()), tk.append(keys[k]), ti.append(c0 + k), tn.append(e[k])
+        gm = max(tm)
+        resc = [torch.exp(m - gm) if torch.isfinite(m) else torch.tensor(0.0, dtype=torch.float64) for m in tm]
+        den = sum(a * b for a, b in zip(ts, resc))
+        rk = [k * r_ if torch.isfinite(m) else -1.0 for k, r_, m in zip(tk, resc, tm)]
+        best = max(range(len(rk)), key=lambda i: (float(rk[i]), -ti[i]))
+        assert ti[best] == int(tok_ref[r])
+        assert abs(float(tn[best] * resc[best] / den) - float(q_ref[r])) <= 1e-6 * float(q_ref[r])
+
+
+def test_sample_step_invalid_rows_and_ties():
+    inf = float("inf")
+    x = torch.tensor([[0.0, 1.0, 1.0, -inf],       # tie between 1 and 2 with equal noise -> 1
+                      [0.0, float("nan"), 1.0, 2.0],  # NaN logit: invalid
+                      [0.0, inf, 1.0, 2.0],        # +inf logit: invalid
+                      [-inf, -inf, -inf, -inf],    # no finite entry: invalid
+                      [0.0, 1.0, 2.0, 3.0],        # T = 0: invalid
+                      [0.0, 1.0, 2.0, 3.0],        # zero noise at a finite entry: invalid
+                      [0.0, 1.0, 2.0, -inf]])      # zero noise at a masked entry: valid
+    t = torch.tensor([1.0, 1.0, 1.0, 1.0, 0.0, 1.0, 1.0])
+    noise = torch.ones(7, 4)
+    noise[5, 2] = 0.0
+    noise[6, 3] = 0.0
+    tokens, q, valid = ov.sample_step_tokens_with_q(x, t, noise)
+    assert valid.tolist() == [True, False, False, False, False, False, True]
+    assert tokens.tolist() == [1, 0, 0, 0, 0, 0, 2]
+    assert bool(torch.isnan(q[1:6]).all())
+    assert abs(float(q[0]) - float(torch.softmax(torch.tensor([0.0, 1.0, 1.0]), 0)[1])) < 1e-7
