@@ -420,6 +420,18 @@ LS_API int ls_finalize_verify_outputs(const void* candidates, int32_t candidates
                                       int64_t prefix_stride, int64_t batch, int32_t width, int64_t* out_tokens,
                                       int32_t* committed, void* next_lengths, void* stream);
 
+/* Committed verify rows into the request-to-token map: replaces
+ * SRT/speculative/draft_free_kv_info.py:32-82 (_assign_fixed_verify_cache_locs).
+ * For request b and i < commit_lens[b] (clamped to [0, width]):
+ * req_to_token[req_pool_indices[b] * rtt_stride + start_offset[b] + i] =
+ * verify_cache_locs[b * locs_stride_b + i]; positions outside [0, pool_len)
+ * are skipped.  Index tensors int32/int64; req_to_token int32. */
+LS_API int ls_assign_verify_cache_locs(const void* req_pool_indices, int32_t slots_dtype, const void* start_offset,
+                                       int32_t start_dtype, const void* commit_lens, int32_t commit_dtype,
+                                       const void* verify_cache_locs, int32_t locs_dtype, int64_t locs_stride_b,
+                                       int32_t* req_to_token, int64_t rtt_stride, int64_t pool_len, int64_t batch,
+                                       int32_t width, void* stream);
+
 /* ---------------------------------------------------------------------------
  * Drafter proposal step: replaces
  * SRT/speculative/dspark_components/kernels/sample_step_tokens_with_q.py:72-382

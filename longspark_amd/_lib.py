@@ -128,6 +128,7 @@ _SIGNATURES = {
     "ls_chain_speculative_sampling": (I32, [ctypes.POINTER(ChainSamplingArgs), P, U64, P, U64, P]),
     "ls_finalize_verify_outputs": (I32, [P, I32, I64, I64, P, I32, I64, P, I32, I64, P, I32, I64, I64, I32, P, P, P,
                                          P]),
+    "ls_assign_verify_cache_locs": (I32, [P, I32, P, I32, P, I32, P, I32, I64, P, I64, I64, I64, I32, P]),
     "ls_sample_step_workspace": (I32, [I64, I64, P, P]),
     "ls_sample_step": (I32, [P, I32, I64, I64, I64, P, P, I64, P, P, P, P, U64, P, U64, P]),
     "ls_raw_page_table": (I32, [P, I64, I64, P, I32, P, I32, I64, I32, P, I64, P, P]),

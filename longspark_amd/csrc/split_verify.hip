@@ -451,6 +451,39 @@ __global__ __launch_bounds__(kCT) void chain_kernel(ChainArgs a) {
   if (lane == 0) a.anum[b] = len;
 }
 
+// Committed cache rows into the request-to-token map: for request b and
+// i < commit_lens[b] (clamped to [0, width]), req_to_token[slot_b, start_b + i]
+// = cache_locs[b, i] (positions past pool_len are skipped).
+struct AssignArgs {
+  const void* slots;
+  int slots_dtype;
+  const void* start;
+  int start_dtype;
+  const void* commit;
+  int commit_dtype;
+  const void* locs;
+  int locs_dtype;
+  int64_t locs_stride_b;
+  int32_t* rtt;
+  int64_t rtt_stride;
+  int64_t pool_len;
+  int64_t batch;
+  int width;
+};
+
+__global__ __launch_bounds__(kST) void assign_cache_locs_kernel(AssignArgs a) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kST + threadIdx.x;
+  if (i >= a.batch * a.width) return;
+  const int64_t b = i / a.width;
+  const int j = static_cast<int>(i - b * a.width);
+  const int64_t n = ld_idx(a.commit, a.commit_dtype, b);
+  if (j >= n) return;
+  const int64_t pos = ld_idx(a.start, a.start_dtype, b) + j;
+  if (pos < 0 || pos >= a.pool_len) return;
+  const int64_t slot = ld_idx(a.slots, a.slots_dtype, b);
+  a.rtt[slot * a.rtt_stride + pos] = static_cast<int32_t>(ld_idx(a.locs, a.locs_dtype, b * a.locs_stride_b + j));
+}
+
 inline bool is_index(int d) { return d == LS_I32 || d == LS_I64; }
 
 inline uint64_t chain_up256(uint64_t x) { return (x + 255) & ~uint64_t(255); }
@@ -572,6 +605,28 @@ extern "C" int ls_chain_speculative_sampling(const ls_chain_sampling_args* args,
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (vec) chain_kernel<true><<<grid, kCT, 0, st>>>(a);
   else chain_kernel<false><<<grid, kCT, 0, st>>>(a);
+  LS_LAUNCH_CHECK();
+  return LS_OK;
+}
+
+extern "C" int ls_assign_verify_cache_locs(const void* req_pool_indices, int32_t slots_dtype, const void* start_offset,
+                                           int32_t start_dtype, const void* commit_lens, int32_t commit_dtype,
+                                           const void* verify_cache_locs, int32_t locs_dtype, int64_t locs_stride_b,
+                                           int32_t* req_to_token, int64_t rtt_stride, int64_t pool_len,
+                                           int64_t batch, int32_t width, void* stream) {
+  using namespace ls;
+  LS_CHECK(batch >= 0 && width >= 1 && pool_len >= 0 && rtt_stride >= pool_len && locs_stride_b >= width,
+           LS_ERR_SHAPE, "ls_assign_verify_cache_locs: bad sizes");
+  LS_CHECK(is_index(slots_dtype) && is_index(start_dtype) && is_index(commit_dtype) && is_index(locs_dtype),
+           LS_ERR_DTYPE, "ls_assign_verify_cache_locs: index tensors must be int32/int64");
+  if (batch == 0) return LS_OK;
+  LS_CHECK(req_pool_indices && start_offset && commit_lens && verify_cache_locs && req_to_token, LS_ERR_VALUE,
+           "ls_assign_verify_cache_locs: null pointer");
+  AssignArgs a{req_pool_indices, slots_dtype, start_offset, start_dtype, commit_lens, commit_dtype,
+               verify_cache_locs, locs_dtype, locs_stride_b, req_to_token, rtt_stride, pool_len, batch, width};
+  const int64_t n = batch * width;
+  assign_cache_locs_kernel<<<dim3(static_cast<unsigned>((n + kST - 1) / kST)), kST, 0,
+                             static_cast<hipStream_t>(stream)>>>(a);
   LS_LAUNCH_CHECK();
   return LS_OK;
 }

@@ -61,6 +61,9 @@ def replacements() -> Dict[str, Dict[str, object]]:
         "sglang.srt.speculative.draft_free_kv_utils": {
             "build_greedy_verify_out_tokens": verify.build_greedy_verify_out_tokens},
         "sglang.srt.speculative.draft_free_kv_dispatch": {"finalize_verify_outputs": verify.finalize_verify_outputs},
+        # committed verify rows into req_to_token (SPEC/draft_free_kv_info.py:32-82)
+        "sglang.srt.speculative.draft_free_kv_info": {
+            "_assign_fixed_verify_cache_locs_func": verify.assign_fixed_verify_cache_locs},
         # vocabulary bitmask (SRT/constrained/triton_ops/bitmask_ops.py:84-141)
         "sglang.srt.constrained.triton_ops.bitmask_ops": {
             "apply_token_bitmask_inplace_triton": penalties.apply_token_bitmask_inplace},

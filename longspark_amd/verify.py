@@ -234,6 +234,30 @@ def finalize_verify_outputs(*, candidates, accept_lens, bonus, prefix_lens):
     return _finalize(candidates, accept_lens, bonus, prefix_lens, "finalize_verify_outputs", True)
 
 
+def assign_fixed_verify_cache_locs(*, req_pool_indices: torch.Tensor, req_to_token: torch.Tensor,
+                                   start_offset: torch.Tensor, commit_lens: torch.Tensor,
+                                   verify_cache_locs: torch.Tensor, batch_size: int, verify_width: int) -> None:
+    """SRT/speculative/draft_free_kv_info.py:62-82 (``_assign_fixed_verify_cache_locs_func``):
+    in place, ``req_to_token[slot_b, start_b + i] = verify_cache_locs[b, i]``
+    for ``i < commit_lens[b]``."""
+    what = "assign_fixed_verify_cache_locs"
+    if verify_cache_locs.shape != (batch_size, verify_width):
+        raise ValueError("fixed verify cache locations have the wrong shape")
+    dev = _lib.require_cuda(req_pool_indices, req_to_token, start_offset, commit_lens, verify_cache_locs, what=what)
+    if req_to_token.dtype != torch.int32 or req_to_token.ndim != 2 or req_to_token.stride(1) != 1:
+        raise ValueError(f"{what}: req_to_token must be int32 [slots, pool_len] with unit column stride")
+    for name, t in (("req_pool_indices", req_pool_indices), ("start_offset", start_offset),
+                    ("commit_lens", commit_lens)):
+        if t.shape != (batch_size,):
+            raise ValueError(f"{what}: {name} must have one entry per request")
+    idx = [t.contiguous() for t in (req_pool_indices, start_offset, commit_lens)]
+    locs = verify_cache_locs if verify_cache_locs.stride(1) == 1 else verify_cache_locs.contiguous()
+    _lib.call("ls_assign_verify_cache_locs", idx[0].data_ptr(), _lib.dtype_code(idx[0]), idx[1].data_ptr(),
+              _lib.dtype_code(idx[1]), idx[2].data_ptr(), _lib.dtype_code(idx[2]), locs.data_ptr(),
+              _lib.dtype_code(locs), locs.stride(0), req_to_token.data_ptr(), req_to_token.stride(0),
+              req_to_token.shape[1], batch_size, verify_width, _lib.stream_of(dev))
+
+
 def build_greedy_verify_out_tokens(*, candidates, accept_lens, bonus):
     """SRT/speculative/draft_free_kv_utils.py:386-408: the ``[B, W]`` int64 committed-token buffer."""
     if candidates.ndim != 2 or accept_lens.shape != (candidates.shape[0],):

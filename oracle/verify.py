@@ -530,3 +530,20 @@ def sample_step_tokens_with_q(step_logits, temperatures, exp_noise, *, compute_d
     q = torch.where(valid, q, torch.full_like(q, float("nan"))).float()
     return tokens, q, valid
 
+
+
+def assign_fixed_verify_cache_locs(req_pool_indices, req_to_token, start_offset, commit_lens, verify_cache_locs):
+    """SPEC/draft_free_kv_info.py:32-59 restated: a copy of ``req_to_token``
+    with ``[slot_b, start_b + i] = verify_cache_locs[b, i]`` for
+    ``i < commit_lens[b]``.  A commit length above the verify width is clamped
+    to it and positions outside the map are skipped (the reference leaves
+    both to the caller's contract)."""
+    out = req_to_token.clone()
+    width = verify_cache_locs.shape[1]
+    for b in range(req_pool_indices.numel()):
+        n = min(max(int(commit_lens[b]), 0), width)
+        for i in range(n):
+            pos = int(start_offset[b]) + i
+            if 0 <= pos < out.shape[1]:
+                out[int(req_pool_indices[b]), pos] = int(verify_cache_locs[b, i])
+    return out

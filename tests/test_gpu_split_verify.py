@@ -100,3 +100,25 @@ def test_finalize_outputs(dev, dtypes):
     greedy = verify.build_greedy_verify_out_tokens(candidates=cand.to(dev), accept_lens=lens.to(dev),
                                                    bonus=bonus.to(dev))
     assert torch.equal(greedy.cpu(), ro)
+
+
+@pytest.mark.parametrize("idx_dtype", [torch.int64, torch.int32])
+def test_assign_fixed_verify_cache_locs(dev, idx_dtype):
+    g = torch.Generator().manual_seed(41)
+    bs, width, slots, pool = 9, 16, 12, 300
+    rtt = torch.randint(0, 1 << 20, (slots, pool), generator=g, dtype=torch.int32)
+    req = torch.randperm(slots, generator=g)[:bs]
+    start = torch.randint(0, pool - width, (bs,), generator=g)
+    start[3] = pool - 5                                 # commit runs past the map: the rest is skipped
+    commit = torch.randint(0, width + 1, (bs,), generator=g)
+    commit[0], commit[1] = 0, width
+    locs = torch.randint(0, 1 << 24, (bs, width), generator=g)
+    print(f"assign verify cache locs {idx_dtype}", flush=True)
+    want = ov.assign_fixed_verify_cache_locs(req, rtt, start, commit, locs)
+    got = rtt.to(dev)
+    verify.assign_fixed_verify_cache_locs(req_pool_indices=req.to(idx_dtype).to(dev), req_to_token=got,
+                                          start_offset=start.to(idx_dtype).to(dev),
+                                          commit_lens=commit.to(torch.int32).to(dev),
+                                          verify_cache_locs=locs.to(dev), batch_size=bs, verify_width=width)
+    torch.cuda.synchronize()
+    assert torch.equal(got.cpu(), want)

@@ -314,3 +314,14 @@ def test_sample_step_invalid_rows_and_ties():
     assert tokens.tolist() == [1, 0, 0, 0, 0, 0, 2]
     assert bool(torch.isnan(q[1:6]).all())
     assert abs(float(q[0]) - float(torch.softmax(torch.tensor([0.0, 1.0, 1.0]), 0)[1])) < 1e-7
+
+
+def test_assign_fixed_verify_cache_locs_hand_case():
+    rtt = torch.zeros(3, 8, dtype=torch.int32)
+    locs = torch.tensor([[10, 11, 12], [20, 21, 22]])
+    out = ov.assign_fixed_verify_cache_locs(torch.tensor([2, 0]), rtt, torch.tensor([1, 6]), torch.tensor([2, 3]),
+                                            locs)
+    # request 0 -> slot 2, positions 1-2; request 1 -> slot 0, positions 6-7 (8 is past the map)
+    assert out[2].tolist() == [0, 10, 11, 0, 0, 0, 0, 0]
+    assert out[0].tolist() == [0, 0, 0, 0, 0, 0, 20, 21]
+    assert int(out[1].abs().sum()) == 0 and int(rtt.abs().sum()) == 0
