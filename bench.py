@@ -576,6 +576,117 @@ class SampleStep:
                 "sample": f"{b} rows, oracle torch-CPU exponential race, median of {k} runs"}
 
 
+class FullRound:
+    """One verify-and-refresh round at Qwen3-14B geometry: 40 layers, 40 query
+    and 8 KV heads, head_dim 128, vocab 151,936, batch 128, block 16, contexts
+    U[8K, 32K] in a paged bf16 cache (page 16).  A round runs the penalty
+    tables and the fused stochastic verify (T 0.7, top-k 50, top-p 0.95,
+    repetition 1.05 over a 2048-token Zipf history), the 256-token window
+    gather of every layer, and the summary update (52 rows per query head,
+    260 per KV head) with each request's committed rows (accepted drafts plus
+    the bonus) read from the cache.  The cache pool holds the pages the
+    windows touch plus as many distractor pages; page-table entries outside
+    the windows alias random pool pages (the values are random, so the access
+    pattern is kept), since 128 contexts of this size do not fit in HBM."""
+
+    name = "full_round"
+    metric = "per-round GB/s (algorithmic bytes): verify + window gather + summary update, Qwen3-14B, B=128"
+    unit = "GB/s"
+    dtype = "bf16"
+
+    def __init__(self, dev, batch=128, width=16, layers=40, q_heads=40, kv_heads=8, dim=128, rows=52, page=16,
+                 window=256):
+        self.verify = StochasticVerify(dev, batch=batch, width=width)
+        self.batch, self.width, self.layers, self.dim, self.window, self.page = batch, width, layers, dim, window, page
+        self.q_heads, self.kv_heads, self.rows = q_heads, kv_heads, rows
+        g = torch.Generator(device=dev).manual_seed(91)
+        ctx = torch.randint(8192, 32769, (batch,), generator=g, device=dev)
+        pages_per = 32768 // page
+        win_pages = window // page + 1
+        pool_pages = 2 * batch * win_pages
+        table = torch.randint(0, pool_pages, (batch, pages_per), generator=g, device=dev, dtype=torch.int32)
+        own = torch.randperm(pool_pages, generator=g, device=dev)[:batch * win_pages].view(batch, win_pages)
+        cols = ((ctx - window) // page)[:, None] + torch.arange(win_pages, device=dev)[None, :]
+        table.scatter_(1, cols.clamp(max=pages_per - 1), own.to(torch.int32))
+        self.table, self.seq = table, ctx
+        n = pool_pages * page
+        self.k = [torch.randn(n, kv_heads, dim, generator=g, device=dev).to(torch.bfloat16) for _ in range(layers)]
+        self.v = [torch.randn(n, kv_heads, dim, generator=g, device=dev).to(torch.bfloat16) for _ in range(layers)]
+        self.out = torch.empty(batch, layers, 2, kv_heads, window, dim, dtype=torch.bfloat16, device=dev)
+        # committed rows: the last `width` positions of each context
+        pos = ctx[:, None] - width + torch.arange(width, device=dev)[None, :]
+        self.locs = table.gather(1, (pos // page)).long() * page + pos % page
+        self.query = torch.randn(layers, q_heads, rows, dim, generator=g, device=dev).to(torch.bfloat16)
+        self.state = torch.randn(batch, layers, q_heads, rows, dim, generator=g, device=dev)
+        self.lse = torch.randn(batch, layers, q_heads, rows, generator=g, device=dev)
+        self.committed = width * batch
+        self._set_bytes(self.verify.rows * V * 2 + batch * V * 4)
+        self.kernel = "full round (all kernels of the round)"
+
+    def _set_bytes(self, verify_bytes):
+        gather = 2 * self.out.numel() * 2
+        summary = (2 * self.state.numel() * 4 + 2 * self.lse.numel() * 4 + self.query.numel() * 2
+                   + self.committed * self.layers * 2 * self.kv_heads * self.dim * 2)
+        self.parts = {"verify": verify_bytes, "window_gather": gather, "summary_update": summary}
+        self.bytes = sum(self.parts.values())
+        self.units = self.bytes / 1e9
+
+    def step(self):
+        from longspark_amd import kvwindow, summary
+        acc, _ = self.verify.step()
+        kvwindow.gather_window(self.k, self.v, self.table, self.seq, page_size=self.page, window=self.window,
+                               out=self.out)
+        lens = (acc + 1).clamp_(0, self.width)   # committed rows: accepted drafts + the bonus
+        summary.summary_update(query=self.query, key_cache=self.k, value_cache=self.v, accepted_cache_locs=self.locs,
+                               accept_lens=lens, state_output=self.state, state_lse=self.lse,
+                               softmax_scale=self.dim ** -0.5)
+        return acc, lens
+
+    def count_rejected(self, out):
+        acc, lens = out
+        self.verify.count_rejected((acc, None))
+        self.committed = int(lens.sum().item())
+        self._set_bytes(self.verify.kernel_bytes + self.batch * self.verify.cfg["history_len"] * 4)
+
+    def config(self):
+        return {"workload": f"full round, Qwen3-14B geometry: verify B={self.batch} K={self.width} V={V} bf16 "
+                            f"(T 0.7, top-k 50, top-p 0.95, repetition 1.05, 2048-token history) + window gather "
+                            f"{self.window} x {self.layers} layers x {self.kv_heads} KV heads x D {self.dim} "
+                            f"(contexts U[8K, 32K], page {self.page}) + summary update "
+                            f"{self.q_heads}x{self.rows} rows per layer over the committed rows",
+                "batch": self.batch, "block": self.width, "vocab": V, "layers": self.layers,
+                "committed_rows": self.committed,
+                "bytes_per_part": self.parts}
+
+    def cpu_baseline(self, threads):
+        from oracle import kvwindow as okw
+        from oracle import summary as osm
+        verify = self.verify.cpu_baseline(threads)       # B=2 requests
+        t_verify = 2 * self.width / verify["rows_per_s"]
+        g = torch.Generator().manual_seed(9)
+        ctx = 4096
+        table = torch.randperm(ctx // self.page, generator=g).to(torch.int32)[None]
+        k = torch.randn(self.layers, ctx, self.kv_heads, self.dim, generator=g).to(torch.bfloat16)
+        v = torch.randn(self.layers, ctx, self.kv_heads, self.dim, generator=g).to(torch.bfloat16)
+        t_gather, _ = time_cpu(lambda: okw.gather_window(k, v, table, torch.tensor([ctx]), self.page, self.window))
+        q = torch.randn(self.layers, self.q_heads, self.rows, self.dim, generator=g).to(torch.bfloat16)
+        kn = torch.randn(self.layers, 1, self.width, self.kv_heads, self.dim, generator=g).to(torch.bfloat16)
+        st = torch.randn(1, self.layers, self.q_heads, self.rows, self.dim, generator=g)
+        ls = torch.randn(1, self.layers, self.q_heads, self.rows, generator=g)
+        lens = torch.full((1,), self.width, dtype=torch.int32)
+
+        def run():
+            for layer in range(self.layers):
+                sc = osm.position_scores(q[layer][None], kn[layer], self.dim ** -0.5)
+                osm.merge_accepted_positions(st[:, layer], ls[:, layer], sc, kn[layer], lens)
+        t_summary, n = time_cpu(run)
+        per_request = self.bytes / self.batch
+        t = t_verify / 2 + t_gather + t_summary
+        return {"value": per_request / t / 1e9, "threads": threads,
+                "sample": f"one request's round: oracle verify (timed at B=2), gather ({self.layers} layers, "
+                          f"context {ctx}) and summary update ({self.layers} layers), torch-CPU, median of {n} runs"}
+
+
 class _BatchInfo(SimpleNamespace):
     """The sampling-info fields the verify logit adjustments read (one entry per request)."""
 
@@ -634,7 +745,7 @@ class AdjustLogits:
 
 
 WORKLOADS = {w.name: w for w in (GreedyVerify, StochasticVerify, WindowGather, SummaryUpdate, SoftmaxTempWorkload,
-                                  TargetProbsWorkload, ChainSampling, AdjustLogits, SampleStep, HbmCopy)}
+                                  TargetProbsWorkload, ChainSampling, AdjustLogits, SampleStep, FullRound, HbmCopy)}
 DEFAULT_WORKLOAD = "verify_sample"
 
 
