@@ -41,7 +41,7 @@ TRAFFIC = {
     "greedy_verify_kernel": (622_640_864, "profiles/greedy_verify_kernel_B128_K16_V151936.md"),
     "window_gather_kernel": (604_246_324, "profiles/window_gather_kernel_B8_L36_Hkv8_D128_ctx131072.md"),
     "summary_kernel": (646_838_203, "profiles/summary_kernel_B8_L36_R256_W16.md"),
-    "softmax_temp_kernel": (2_454_199_302, "profiles/softmax_temp_kernel_B128_K16_V151936.md"),
+    "softmax_temp_kernel": (2_383_427_050, "profiles/softmax_temp_kernel_B128_K16_V151936.md"),
     "chain_kernel": (158_497_097, "profiles/chain_kernel_chain_sampling_B128_K16_V151936.md"),
     "request_bias_kernel": (1_403_662_037, "profiles/request_bias_kernel_adjust_logits_B128_K16_V151936.md"),
     "sample_step_kernel": (156_653_721, "profiles/sample_step_kernel_B128_V151936.md"),

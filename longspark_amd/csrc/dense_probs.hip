@@ -132,7 +132,11 @@ __global__ __launch_bounds__(kST) void softmax_temp_kernel(const typename Tag::s
   if constexpr (kVec) {
     constexpr int kU = sizeof(S) == 2 ? 2 * kSTU : kSTU;  // 8-byte loads: twice as many in flight
     const int64_t n4 = vocab / 4;
-    for (int64_t v0 = tid; v0 < n4; v0 += kU * kST) {
+    // last chunk first: the end of the row was read last in the first pass,
+    // so more of it is still in the L2
+    const int64_t steps = (n4 + kU * kST - 1) / (kU * kST);
+    for (int64_t it = steps - 1; it >= 0; --it) {
+      const int64_t v0 = it * (kU * kST) + tid;
       float x[kU][4];
 #pragma unroll
       for (int u = 0; u < kU; ++u) load4_stream<Tag>(rp + min<int64_t>(v0 + u * kST, n4 - 1) * 4, x[u]);

@@ -286,6 +286,7 @@ extern "C" int ls_sample_step(const void* logits, int32_t logits_dtype, int64_t 
   if (tpw < 1) tpw = 1;
   a.tps = static_cast<int>(tpw);
   a.slices = static_cast<int>((a.ntiles + kSSWaves * tpw - 1) / (kSSWaves * tpw));
+  LS_CHECK(rows * a.slices < (int64_t(1) << 31), LS_ERR_SHAPE, "ls_sample_step: rows x vocab too large for one launch");
   const dim3 grid(static_cast<unsigned>(rows * a.slices));
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool nvec = aligned16(exp_noise) && noise_row_stride % 4 == 0;
