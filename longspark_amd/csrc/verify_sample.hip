@@ -1894,31 +1894,46 @@ constexpr uint64_t kAccPublished = uint64_t(1) << 63;
 // the request's draft row then goes to the exact pass in resolve.
 constexpr int kPollLimit = 1 << 19;
 
-// Accepted length of request b for a draft slice of the fused launch: walks
-// the drafted positions in order, waiting for each target row's acceptance
-// word, and stops at the first rejection (width-1: none), so a request that
-// rejects early waits only for the rows up to the rejection.  -1: not decided
+// Accepted length of request b for a draft slice of the fused launch: the
+// first rejection among the drafted positions (width-1: none), waiting only
+// for the target rows up to it, so a request that rejects early waits only
+// for the rows up to the rejection.  -1: not decided
 // here (a row up to the rejection went to the exact fallback, or the wait
 // limit passed).  qv / uv: lane j's draft probability and uniform of
 // position j (width <= 64, so one position per lane).
 __device__ __forceinline__ int fused_accept_length(const Args& a, int64_t b, float qv, float uv) {
   const int g = a.width - 1;
+  const int lane = threadIdx.x & (kWave - 1);
   const uint64_t* acc = a.acc_t + b * a.width;
+  // Positions below j are accepted.  The words of positions j.. are read at
+  // once (lane k: position k), so a request whose rows are done is decided in
+  // one round trip; while the first undecided position is unpublished only
+  // its word is polled, then the rest are read at once again.
   int j = 0;
-  for (int it = 0; it < kPollLimit && j < g; ++it) {
-    const uint64_t w0 = atomic_peek_u64(acc + j);  // one address: one load for the wave
-    const uint64_t w = (static_cast<uint64_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(w0 >> 32))) << 32) |
-                       __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(w0));
-    if (!(w & kAccPublished)) {
+  bool all = true;
+  for (int it = 0; it < kPollLimit; ++it) {
+    const bool mine = all ? (lane >= j && lane < g) : lane == j;
+    const uint64_t w = mine ? atomic_peek_u64(acc + lane) : 0;
+    const bool pub = (w & kAccPublished) != 0;
+    const bool ovf = pub && (static_cast<uint32_t>(w >> 32) & kFlagOverflow);
+    const bool rej = pub && !ovf && !(uv * qv < __uint_as_float(static_cast<uint32_t>(w)));
+    const uint64_t stop = __ballot(mine && (!pub || ovf || rej));
+    if (!stop) {
+      if (all) return g;
+      if (++j >= g) return g;  // the polled position was accepted
+      all = true;
+      continue;
+    }
+    const int k = __ffsll(static_cast<long long>(stop)) - 1;
+    if (!__shfl(static_cast<int>(pub), k, kWave)) {
+      j = k;
+      all = false;
       __builtin_amdgcn_s_sleep(8);
       continue;
     }
-    if (static_cast<uint32_t>(w >> 32) & kFlagOverflow) return -1;
-    const float q = __shfl(qv, j, kWave), u = __shfl(uv, j, kWave);
-    if (!(u * q < __uint_as_float(static_cast<uint32_t>(w)))) return j;
-    ++j;
+    return __shfl(static_cast<int>(ovf), k, kWave) ? -1 : k;
   }
-  return j < g ? -1 : g;
+  return -1;
 }
 
 // One draft slice (one wavefront) of request b.  kFused: the slice runs in
