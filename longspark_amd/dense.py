@@ -40,6 +40,8 @@ def softmax_temp(*, logits: torch.Tensor, temperatures: torch.Tensor, rows_per_r
     x = _rows(logits, what)
     temps = temperatures.reshape(bs).to(device=dev, dtype=torch.float32).contiguous()
     out = torch.empty((num_rows, vocab), dtype=torch.float32, device=dev)
+    if num_rows == 0:
+        return out
     _lib.call("ls_softmax_temp", x.data_ptr(), _lib.dtype_code(x), x.stride(0), num_rows, vocab, temps.data_ptr(),
               rows_per_request, out.data_ptr(), out.stride(0), _lib.stream_of(dev))
     return out
@@ -93,6 +95,8 @@ def target_probs(*, logits: torch.Tensor, temperatures: torch.Tensor, rows_per_r
     ps = per_request(top_ps, torch.float32, "top_ps")
     mps = per_request(min_ps, torch.float32, "min_ps")
     out = torch.empty((rows, vocab), dtype=torch.float32, device=dev)
+    if rows == 0:
+        return out
     status = torch.empty(1, dtype=torch.int32, device=dev)  # cleared by the call's first kernel
     mk = 0 if max_top_k is None else int(max_top_k)
     a = _lib.TargetProbsArgs()

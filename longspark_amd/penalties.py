@@ -65,9 +65,10 @@ def build_penalty_tables(history: torch.Tensor, vocab: int, *, frequency=None, p
     frequency, presence, repetition = vec(frequency, "frequency"), vec(presence, "presence"), vec(repetition, "repetition")
     if history_lens is not None:
         history_lens = history_lens.to(torch.int32).contiguous()
-    _lib.call("ls_penalty_tables", history.data_ptr(), history.stride(0), _lib.ptr(history_lens), batch, cap, vocab,
-              _lib.ptr(frequency), _lib.ptr(presence), bits.data_ptr(), rank.data_ptr(), words, add.data_ptr(),
-              add.shape[1], distinct.data_ptr(), nonpositive.data_ptr(), _lib.stream_of(dev))
+    if batch > 0:  # an empty batch has empty tables
+        _lib.call("ls_penalty_tables", history.data_ptr(), history.stride(0), _lib.ptr(history_lens), batch, cap,
+                  vocab, _lib.ptr(frequency), _lib.ptr(presence), bits.data_ptr(), rank.data_ptr(), words, add.data_ptr(),
+                  add.shape[1], distinct.data_ptr(), nonpositive.data_ptr(), _lib.stream_of(dev))
     return PenaltyTables(bits=bits, rank=rank, add=add, distinct=distinct, nonpositive=nonpositive,
                          repetition=repetition,
                          verify_quirk=verify_quirk, has_additive=frequency is not None or presence is not None)
@@ -92,6 +93,8 @@ def adjust_logits_(logits: torch.Tensor, *, rows_per_request: int, tables: Optio
         expect = rows // rows_per_request if mask_per_request else rows
         if vocab_mask.shape[0] != expect:
             raise ValueError(f"{what}: vocab_mask has {vocab_mask.shape[0]} rows, expected {expect}")
+    if rows == 0:
+        return
     t = tables
     _lib.call("ls_adjust_logits", logits.data_ptr(), _lib.dtype_code(logits), logits.stride(0), rows, vocab,
               rows_per_request,
@@ -161,6 +164,8 @@ def add_request_bias_(logits: torch.Tensor, *, rows_per_request: int, bias: Opti
         if vocab_mask.dtype != torch.int32 or vocab_mask.ndim != 2 or vocab_mask.shape[0] != batch or \
                 vocab_mask.stride(1) != 1 or vocab_mask.shape[1] > (vocab + 31) // 32:
             raise ValueError(f"{what}: vocab_mask must be int32 [{batch}, <= {(vocab + 31) // 32}]")
+    if rows == 0:
+        return
     _lib.call("ls_add_request_bias", logits.data_ptr(), _lib.dtype_code(logits), logits.stride(0), rows, vocab,
               rows_per_request, _lib.ptr(bias), bias.stride(0) if bias is not None else 0,
               _lib.ptr(vocab_mask), vocab_mask.stride(0) if vocab_mask is not None else 0,

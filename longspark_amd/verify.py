@@ -62,6 +62,8 @@ def verify_greedy(*, logits: torch.Tensor, candidates: torch.Tensor, width: int,
     bonus = torch.empty(batch, dtype=torch.int64, device=dev)
     trim = torch.empty(batch, dtype=torch.int32, device=dev)
     truth = torch.empty(batch * width, dtype=torch.int32, device=dev) if return_truth else None
+    if batch == 0:  # an empty batch: empty outputs, as the reference's tensor code gives
+        return (accept, bonus, trim, truth) if return_truth else (accept, bonus, trim)
     cnt, scr = _lib.workspaces.get(*_lib.workspace_sizes("ls_verify_greedy_workspace", batch, width, vocab),
                                    dev)
     _lib.call("ls_verify_greedy", logits.data_ptr(), _lib.dtype_code(logits), logits.stride(0),
@@ -371,6 +373,13 @@ def verify_sample(*, logits: torch.Tensor, candidates: torch.Tensor, width: int,
     trim = torch.empty(batch, dtype=torch.int32, device=dev) if return_cap_trim else None  # written per request
     bonus = torch.empty(batch, dtype=torch.int64, device=dev)
     p_cand = torch.empty(batch, g, dtype=torch.float32, device=dev) if return_p_cand else None
+    if batch == 0:  # an empty batch: empty outputs, as the reference's tensor code gives
+        out = (accept, bonus)
+        if return_cap_trim:
+            out += (trim,)
+        if return_p_cand:
+            out += (p_cand,)
+        return out
     status = torch.empty(1, dtype=torch.int32, device=dev)  # cleared by the call's first kernel
     a = _lib.VerifySampleArgs()
     a.logits, a.logits_dtype, a.logits_row_stride = logits.data_ptr(), _lib.dtype_code(logits), logits.stride(0)

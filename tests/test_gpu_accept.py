@@ -436,3 +436,38 @@ def test_add_request_bias_combined_mask(dev, dtype, vocab, offset):
     ref = base.clone()
     ref[:, offset:].view(bs, rpr, vocab).add_(z.to(dtype)[:, None, :])
     assert torch.equal(x.cpu(), ref)
+
+
+# ------------------------------------------------------------- empty batches
+
+def test_empty_batches(dev):
+    """Zero-request inputs give empty outputs and launch nothing, as the
+    reference's tensor code does with empty tensors."""
+    from longspark_amd import sample
+    v = 1000
+    print("empty batches", flush=True)
+    logits = torch.empty(0, v, dtype=torch.bfloat16, device=dev)
+    cand = torch.empty(0, 8, dtype=torch.int64, device=dev)
+    acc, bonus, trim = verify.verify_greedy(logits=logits, candidates=cand, width=8)
+    assert acc.shape == (0,) and bonus.shape == (0,) and trim.shape == (0,)
+    z = torch.empty(0, device=dev)
+    acc, bonus, trim, pc = verify.verify_sample(
+        logits=logits, candidates=cand, width=8, temperatures=z, uniforms=torch.empty(0, 7, device=dev),
+        final_uniforms=z, draft_logits=torch.empty(0, 7, v, device=dev),
+        draft_token_probs=torch.empty(0, 7, device=dev), return_cap_trim=True, return_p_cand=True)
+    assert acc.shape == (0,) and bonus.shape == (0,) and trim.shape == (0,) and pc.shape == (0, 7)
+    assert dense.softmax_temp(logits=logits, temperatures=z, rows_per_request=8).shape == (0, v)
+    assert dense.target_probs(logits=logits, temperatures=z, rows_per_request=8, top_ks=torch.empty(0, device=dev),
+                              top_ps=z).shape == (0, v)
+    tables = penalties.build_penalty_tables(torch.empty(0, 16, dtype=torch.int32, device=dev), v,
+                                            repetition=z)
+    assert tables.bits.shape[0] == 0
+    penalties.adjust_logits_(logits, rows_per_request=8, tables=tables)
+    penalties.add_request_bias_(logits, rows_per_request=8, bias=torch.empty(0, v, device=dev))
+    ridx, nxt, sib, preds, aidx, anum = accept.chain_verify_buffers(bs=0, draft_token_num=8, device=dev)
+    accept.chain_speculative_sampling_triton(preds, aidx, anum, cand, ridx, nxt, sib, torch.empty(0, 7, device=dev),
+                                             z, torch.empty(0, 8, v, device=dev), torch.empty(0, 7, v, device=dev),
+                                             1.0, 1.0, True)
+    tok, q = sample.sample_step_tokens_with_q(step_logits=torch.empty(0, v, device=dev), temperatures=z)
+    assert tok.shape == (0,) and q.shape == (0,)
+    torch.cuda.synchronize()
