@@ -260,7 +260,8 @@ typedef struct {
   int32_t* status;
   /* Optional timing: NULL, or 4 hipEvent_t handles recorded on the stream
    * before the target scan, after it, before the resolve kernel and after it
-   * (the middle interval holds the fallback and draft-scan kernels). */
+   * (the middle interval holds the fallback and draft-scan kernels); a NULL
+   * handle is not recorded. */
   void* const* timing_events;
   /* Which row-scan kernels to launch: 0 = both (each row runs in the one for
    * its path), 1 = only the raw-logit top-k scan (for callers that know every

@@ -104,6 +104,7 @@ struct Args {
   int dwave;           // 1: draft_wave_kernel runs (takes draft rows that are top-k with k <= kWaveMaxK)
   int dwave_only;      // 1: no workgroup draft scan follows
   int fuse_draft;      // 1: verify_wave_kernel's grid also carries the draft slices (after the target rows)
+  int inline_fb;       // 1: no target fallback launch; resolve runs the exact pass on the rows it needs
   int dslices;         // wavefront draft slices per request (<= kDraftSlices)
   uint64_t* acc_t;     // [B*K] acceptance word of each target row (fused launch; zero when not published)
   uint32_t* list_cnt;  // counters [2]: rows waiting for the exact fallback (target, draft)
@@ -2212,29 +2213,33 @@ __device__ __noinline__ void write_exact_record(Shared& sh, const Exact& ex, int
   __syncthreads();
 }
 
+// Exact support of one target row the scans could not resolve; rewrites its
+// record and support.  Called by the whole workgroup.
+template <typename TagT>
+__device__ __forceinline__ void target_exact_row(Shared& sh, const Args& a, int64_t row) {
+  const int64_t b = row / a.width;
+  const RowRec prev = a.rec_t[row];
+  Params p{a.temps[b], a.top_ks ? max(a.top_ks[b], 1) : static_cast<int>(a.vocab),
+           a.top_ps ? a.top_ps[b] : 1.f, a.min_ps ? a.min_ps[b] : 0.f};
+  using S = typename TagT::storage;
+  const S* rp = static_cast<const S*>(a.logits) + row * a.lrs;
+  const XForm f = target_xform(a, b, row);
+  const CandRec cr = a.cand_rec[row];
+  const int mode = row_mode(p, a.vocab);
+  float m_x = prev.m;
+  double z = prev.z;
+  if (prev.flags & kFlagUnscanned) row_stats<TagT>(sh, rp, a.vocab, f, p.temperature, &m_x, &z);
+  const Exact ex = exact_support<TagT>(sh, rp, a.vocab, f, p, mode, m_x, z);
+  const int n_f = ex.n <= kCap ? collect<TagT>(sh, rp, a.vocab, f, p.temperature, ex.kcut) : 0;
+  write_exact_record(sh, ex, n_f, a.rec_t + row, a.sidx_t + row * kCap, a.sp_t + row * kCap, cr.tok, cr.x,
+                     p.temperature, prev.why);
+}
+
 template <typename TagT, typename CandT>
 __global__ __launch_bounds__(kT) void target_fallback_kernel(Args a) {
   __shared__ Shared sh;
   const uint32_t n = *a.list_cnt;
-  for (uint32_t li = blockIdx.x; li < n; li += gridDim.x) {
-    const int64_t row = a.list_t[li];
-    const int64_t b = row / a.width;
-    const RowRec prev = a.rec_t[row];
-    Params p{a.temps[b], a.top_ks ? max(a.top_ks[b], 1) : static_cast<int>(a.vocab),
-             a.top_ps ? a.top_ps[b] : 1.f, a.min_ps ? a.min_ps[b] : 0.f};
-    using S = typename TagT::storage;
-    const S* rp = static_cast<const S*>(a.logits) + row * a.lrs;
-    const XForm f = target_xform(a, b, row);
-    const CandRec cr = a.cand_rec[row];
-    const int mode = row_mode(p, a.vocab);
-    float m_x = prev.m;
-    double z = prev.z;
-    if (prev.flags & kFlagUnscanned) row_stats<TagT>(sh, rp, a.vocab, f, p.temperature, &m_x, &z);
-    const Exact ex = exact_support<TagT>(sh, rp, a.vocab, f, p, mode, m_x, z);
-    const int n_f = ex.n <= kCap ? collect<TagT>(sh, rp, a.vocab, f, p.temperature, ex.kcut) : 0;
-    write_exact_record(sh, ex, n_f, a.rec_t + row, a.sidx_t + row * kCap, a.sp_t + row * kCap, cr.tok, cr.x,
-                       p.temperature, prev.why);
-  }
+  for (uint32_t li = blockIdx.x; li < n; li += gridDim.x) target_exact_row<TagT>(sh, a, a.list_t[li]);
 }
 
 // Exact support of request b's draft row at position len (a row the draft
@@ -2579,51 +2584,63 @@ __global__ __launch_bounds__(kT) void resolve_kernel(Args a) {
   // the target support at the accepted length is requested meanwhile.
   int ti = 0;
   float tp = 0.f;
-  if (tid < kWave) {
-    const int lane = tid;
-    const int ns = a.dslices;
-    uint64_t c = 0, mw = 0;  // the slices' codes do not depend on the acceptance: requested first
-    if (a.q_mode == 0 && a.dwave && lane < ns) {
-      const uint64_t* pubs = a.pubs_d + b * 2 * kDraftSlices;
-      c = pubs[2 * lane];
-      mw = pubs[2 * lane + 1];
-    }
-    int fl;
-    const int len = resolve_accept_wave<CandT>(a, b, &s_len, &s_flags, &s_tr, &fl);
-    wave_sync();
-    const RowRec tr = s_tr;
-    if (lane < tr.n) {
-      const int64_t trow = b * a.width + len;
-      ti = a.sidx_t[trow * kCap + lane];
-      tp = a.sp_t[trow * kCap + lane];
-    }
-    int merge = 0;
-    if (len < g && a.q_mode == 0 && !fl && !(tr.flags & kFlagOverflow) && a.dwave) {
-      const Params pd = draft_params(a, b);
-      if (row_mode(pd, a.vocab) == kModeTopK && pd.top_k <= kWaveMaxK) {
-        if (__ballot(lane < ns && c >= kPubSkip && c != kPubBad)) {
-          // a slice could not decide the acceptance: the exact pass, unscanned
-          if (lane == 0) {
-            RowRec rr{};
-            rr.flags = kFlagOverflow | kFlagUnscanned;
-            rr.why = kWhyDefer;
-            a.rec_d[b] = rr;
-          }
-        } else {
-          merge = __ballot(lane < ns && c == kPubBad) ? 2 : 1;
-          if (lane < kDraftSlices) ms.cnt[lane] = (lane < ns && c != kPubBad) ? static_cast<int>(c) : 0;
-          const float rmx = wave_max(lane < ns ? unordered_f32(static_cast<uint32_t>(mw >> 32)) : -FLT_MAX);
-          const float sb = wave_max(lane < ns ? unordered_f32(static_cast<uint32_t>(mw)) : -INFINITY);
-          if (lane == 0) {
-            s_rawmax = rmx;
-            s_sbound = sb;
+  int64_t tried = -1;  // the target row given an exact pass here
+  for (;;) {
+    if (tid < kWave) {
+      const int lane = tid;
+      const int ns = a.dslices;
+      uint64_t c = 0, mw = 0;  // the slices' codes do not depend on the acceptance: requested first
+      if (a.q_mode == 0 && a.dwave && lane < ns) {
+        const uint64_t* pubs = a.pubs_d + b * 2 * kDraftSlices;
+        c = pubs[2 * lane];
+        mw = pubs[2 * lane + 1];
+      }
+      int fl;
+      const int len = resolve_accept_wave<CandT>(a, b, &s_len, &s_flags, &s_tr, &fl);
+      wave_sync();
+      const RowRec tr = s_tr;
+      if (lane < tr.n) {
+        const int64_t trow = b * a.width + len;
+        ti = a.sidx_t[trow * kCap + lane];
+        tp = a.sp_t[trow * kCap + lane];
+      }
+      int merge = 0;
+      if (len < g && a.q_mode == 0 && !fl && !(tr.flags & kFlagOverflow) && a.dwave) {
+        const Params pd = draft_params(a, b);
+        if (row_mode(pd, a.vocab) == kModeTopK && pd.top_k <= kWaveMaxK) {
+          if (__ballot(lane < ns && c >= kPubSkip && c != kPubBad)) {
+            // a slice could not decide the acceptance: the exact pass, unscanned
+            if (lane == 0) {
+              RowRec rr{};
+              rr.flags = kFlagOverflow | kFlagUnscanned;
+              rr.why = kWhyDefer;
+              a.rec_d[b] = rr;
+            }
+          } else {
+            merge = __ballot(lane < ns && c == kPubBad) ? 2 : 1;
+            if (lane < kDraftSlices) ms.cnt[lane] = (lane < ns && c != kPubBad) ? static_cast<int>(c) : 0;
+            const float rmx = wave_max(lane < ns ? unordered_f32(static_cast<uint32_t>(mw >> 32)) : -FLT_MAX);
+            const float sb = wave_max(lane < ns ? unordered_f32(static_cast<uint32_t>(mw)) : -INFINITY);
+            if (lane == 0) {
+              s_rawmax = rmx;
+              s_sbound = sb;
+            }
           }
         }
       }
+      if (lane == 0) s_merge = merge;
     }
-    if (lane == 0) s_merge = merge;
+    __syncthreads();
+    // Without a fallback launch, the target row at the accepted length that
+    // the scans could not resolve gets its exact pass here and the acceptance
+    // is walked again (rows past the first rejection are never needed).
+    if (!(a.inline_fb && s_flags)) break;
+    const int64_t trow = b * a.width + s_len;
+    if (trow == tried) break;  // still unresolved (capacity): the request is blocked
+    tried = trow;
+    target_exact_row<TagT>(sh, a, trow);
+    __syncthreads();
   }
-  __syncthreads();
   RowRec dm{};  // the merged draft record (wave 0)
   const int merge = s_merge;
   if (merge == 1) {
@@ -2846,7 +2863,7 @@ extern "C" int ls_verify_sample(const ls_verify_sample_args* in, void* counters,
   a.s_t = l.s_t;
   a.s_d = l.s_d;
   a.hint = x.scan_hint;
-  a.wave = a.wave_only = a.dwave = a.dwave_only = a.fuse_draft = 0;
+  a.wave = a.wave_only = a.dwave = a.dwave_only = a.fuse_draft = a.inline_fb = 0;
   hipStream_t st = static_cast<hipStream_t>(stream);
 
   const dim3 g_t(static_cast<unsigned>(rows * l.s_t)), g_d(static_cast<unsigned>(x.batch * l.s_d)),
@@ -2855,7 +2872,7 @@ extern "C" int ls_verify_sample(const ls_verify_sample_args* in, void* counters,
   void* const* ev = x.timing_events;
 #define LS_EVENT(i)                                                                              \
   do {                                                                                           \
-    if (hipEventRecord(static_cast<hipEvent_t>(ev[i]), st) != hipSuccess)                        \
+    if (ev[i] && hipEventRecord(static_cast<hipEvent_t>(ev[i]), st) != hipSuccess)               \
       return fail(LS_ERR_LAUNCH, "ls_verify_sample: hipEventRecord failed");                     \
   } while (0)
   const bool tvec_ok = aligned16(x.logits);
@@ -2875,6 +2892,8 @@ extern "C" int ls_verify_sample(const ls_verify_sample_args* in, void* counters,
     a.dwave = (x.q_mode == 0 && a.hint != kHintExactOnly && dv && a.dslices >= kDraftMinSlices) ? 1 : 0;      \
     a.dwave_only = (a.dwave && x.max_top_k > 0 && x.max_top_k <= kWaveMaxRowK) ? 1 : 0;                       \
     a.fuse_draft = (a.wave && a.dwave) ? 1 : 0;                                                               \
+    /* every row on the wavefront paths and no per-row output: resolve takes the exact passes it needs */     \
+    a.inline_fb = (a.fuse_draft && a.wave_only && a.dwave_only && !x.p_cand_out) ? 1 : 0;                     \
     if (ev) LS_EVENT(0);                                                                                      \
     if (a.wave) {                                                                                             \
       const int64_t nwg = rows + (a.fuse_draft ? x.batch * a.dslices : 0);                                    \
@@ -2892,8 +2911,10 @@ extern "C" int ls_verify_sample(const ls_verify_sample_args* in, void* counters,
       LS_LAUNCH_CHECK();                                                                                      \
     }                                                                                                         \
     if (ev) LS_EVENT(1);                                                                                      \
-    target_fallback_kernel<TT, CT><<<g_f, rs::kT, 0, st>>>(a);                                                \
-    LS_LAUNCH_CHECK();                                                                                        \
+    if (!a.inline_fb) {                                                                                       \
+      target_fallback_kernel<TT, CT><<<g_f, rs::kT, 0, st>>>(a);                                              \
+      LS_LAUNCH_CHECK();                                                                                      \
+    }                                                                                                         \
     if (x.q_mode == 0) {                                                                                      \
       if (a.dwave && !a.fuse_draft) {                                                                         \
         draft_wave_kernel<TD, CT><<<dim3(static_cast<unsigned>(x.batch * a.dslices)), kWave, 0, st>>>(a);     \

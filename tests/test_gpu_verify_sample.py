@@ -164,3 +164,40 @@ def test_dense_draft_probs(dev):
     ref_bonus = preds[aidx[torch.arange(4), anum.long()].long()]
     assert torch.equal(acc, anum), (acc, anum)
     assert torch.equal(bonus, ref_bonus.long()), (bonus, ref_bonus)
+
+
+@pytest.mark.parametrize("case", ["ties", "off-raw"])
+def test_inline_exact_pass_matches_fallback_launch(dev, case):
+    # Without the per-row p(drafted) output the fused launch skips the
+    # fallback kernel and the resolve kernel runs the exact pass on the target
+    # rows it needs; the results equal the fallback launch's and the oracle's.
+    if case == "ties":  # integer logits: ties at the top-k threshold overflow the candidate buffers
+        d = workloads.stochastic_inputs(6, 8, seed=24, temperature=1.0, top_k=50, top_p=0.8)
+        g = torch.Generator().manual_seed(24)
+        d["logits"] = torch.randint(-4, 5, d["logits"].shape, generator=g).to(torch.bfloat16)
+        max_top_k = 50
+    else:  # a negative presence penalty sends every row to the exact pass unscanned
+        d = workloads.stochastic_inputs(6, 16, seed=25, temperature=0.9, top_k=64, top_p=0.9, history_len=3000,
+                                        repetition=1.1, presence=-0.7, frequency=0.05)
+        max_top_k = 64
+    print(f"inline exact pass: {case}", flush=True)
+    acc_f, bonus_f, _ = run_kernel(dev, d, scan_hint=1, max_top_k=max_top_k)  # with p_cand: fallback launch
+    p = d["params"]
+    tables = None
+    if "history" in d:
+        tables = penalties.build_penalty_tables(d["history"].to(dev), d["logits"].shape[1],
+                                                frequency=d["frequency"].to(dev), presence=d["presence"].to(dev),
+                                                repetition=d["repetition"].to(dev))
+    acc, bonus = verify.verify_sample(
+        logits=d["logits"].to(dev), candidates=d["candidates"].to(dev), width=d["candidates"].shape[1],
+        temperatures=p.temperatures.to(dev), top_ks=p.top_ks.to(dev), top_ps=p.top_ps.to(dev),
+        min_ps=p.min_ps.to(dev), uniforms=d["uniforms"].to(dev), final_uniforms=d["final_uniforms"].to(dev),
+        draft_logits=d["draft_logits"].to(dev), draft_token_probs=d["draft_token_probs"].to(dev),
+        draft_top_ks=p.top_ks.to(dev), draft_top_ps=p.top_ps.to(dev), draft_min_ps=p.min_ps.to(dev),
+        penalties=tables, check=True, scan_hint=1, max_top_k=max_top_k)
+    torch.cuda.synchronize()
+    assert torch.equal(acc.cpu(), acc_f) and torch.equal(bonus.cpu(), bonus_f), (acc, acc_f, bonus, bonus_f)
+    c = vr.oracle_inputs(d)
+    lens_r, bonus_r, probs_r = vr.run_oracle(c)
+    bad, exempt, msgs = vr.classify(c, acc.cpu(), bonus.cpu(), lens_r, bonus_r, probs_r)
+    assert not bad, msgs
