@@ -37,7 +37,7 @@ V = 151936
 # copy (x2.0 and x1.0).  The commands and raw counter values are in the
 # profiles/ summary named beside each figure.
 TRAFFIC = {
-    "verify_wave_kernel": (712_321_149, "profiles/verify_wave_kernel_verify_sample_B128_K16_V151936.md"),
+    "verify_wave_kernel": (712_314_120, "profiles/verify_wave_kernel_verify_sample_B128_K16_V151936.md"),
     "greedy_verify_kernel": (622_640_864, "profiles/greedy_verify_kernel_B128_K16_V151936.md"),
     "window_gather_kernel": (604_246_324, "profiles/window_gather_kernel_B8_L36_Hkv8_D128_ctx131072.md"),
     "summary_kernel": (646_838_203, "profiles/summary_kernel_B8_L36_R256_W16.md"),
