@@ -587,6 +587,65 @@ class SampleStep:
                 "sample": f"{b} rows, oracle torch-CPU exponential race, median of {k} runs"}
 
 
+class Global16Prefill:
+    """Prefill summary initialisation (run_prefill_global_attention of every
+    selected layer) at Qwen3-14B geometry: 5 selected layers, 40 query and 8
+    KV heads, 16 summary slots, head_dim 128, one request with a 131,072-token
+    prefix in bf16 pools of page size 1, the prefix's locations a random
+    permutation of 16-token pages.  All five layers go in one launch (plus the
+    split combine)."""
+
+    name = "global16_prefill"
+    metric = "prefill summary initialisation GB/s (algorithmic bytes) at 5L x 8 Hkv x D128, prefix 131072, B 1"
+    unit = "GB/s"
+    dtype = "bf16"
+
+    def __init__(self, dev, batch=1, layers=5, q_heads=40, kv_heads=8, rows=16, dim=128, prefix=131072, page=16):
+        self.batch, self.layers, self.q_heads, self.kv_heads = batch, layers, q_heads, kv_heads
+        self.rows, self.dim, self.prefix = rows, dim, prefix
+        g = torch.Generator(device=dev).manual_seed(57)
+        n = batch * prefix
+        pages = torch.randperm(n // page, generator=g, device=dev).view(batch, prefix // page)
+        self.table = (pages[:, :, None] * page + torch.arange(page, device=dev)).view(batch, prefix).to(torch.int32)
+        self.lens = torch.full((batch,), prefix, dtype=torch.int32, device=dev)
+        self.k = [torch.randn(n, kv_heads, dim, generator=g, device=dev).to(torch.bfloat16) for _ in range(layers)]
+        self.v = [torch.randn(n, kv_heads, dim, generator=g, device=dev).to(torch.bfloat16) for _ in range(layers)]
+        self.query = torch.randn(layers, q_heads, rows, dim, generator=g, device=dev).to(torch.bfloat16)
+        self.out = torch.empty(batch, layers, q_heads, rows, dim, device=dev)
+        self.lse = torch.empty(batch, layers, q_heads, rows, device=dev)
+        kv = 2 * layers * batch * prefix * kv_heads * dim * 2
+        self.bytes = kv + self.query.numel() * 2 + self.out.numel() * 4 + self.lse.numel() * 4 + batch * prefix * 4
+        self.units = self.bytes / 1e9
+        self.kernel = "prefill_kernel + prefill_combine_kernel"
+
+    def step(self):
+        from longspark_amd import summary
+        return summary.prefill_global_attention(query=self.query, key_cache=self.k, value_cache=self.v,
+                                                page_table=self.table, cache_seqlens=self.lens,
+                                                softmax_scale=self.dim ** -0.5, output=self.out, lse=self.lse)
+
+    def config(self):
+        return {"workload": f"Global16 prefill B={self.batch} L={self.layers} Hq={self.q_heads} x S={self.rows} "
+                            f"Hkv={self.kv_heads} D={self.dim} prefix {self.prefix}, bf16 K/V, page size 1 "
+                            "(16-token pages permuted)", "batch": self.batch}
+
+    def cpu_baseline(self, threads):
+        from oracle import summary as osm
+        torch.set_num_threads(threads)
+        n = 8192             # per-token work is the same at every prefix length
+        g = torch.Generator().manual_seed(8)
+        q = torch.randn(self.q_heads, self.rows, self.dim, generator=g).to(torch.bfloat16)
+        k = torch.randn(n, self.kv_heads, self.dim, generator=g).to(torch.bfloat16)
+        v = torch.randn(n, self.kv_heads, self.dim, generator=g).to(torch.bfloat16)
+        table = torch.randperm(n, generator=g)[None].to(torch.int32)
+        lens = torch.tensor([n], dtype=torch.int32)
+        med, reps = time_cpu(lambda: osm.prefill_global_attention(q, k, v, table, lens, self.dim ** -0.5,
+                                                                   dtype=torch.float32))
+        per_layer = 2 * n * self.kv_heads * self.dim * 2
+        return {"value": per_layer / med / 1e9, "threads": threads,
+                "sample": f"one layer, prefix {n}, oracle torch-CPU fp32 attention, median of {reps} runs"}
+
+
 class FullRound:
     """One verify-and-refresh round at Qwen3-14B geometry: 40 layers, 40 query
     and 8 KV heads, head_dim 128, vocab 151,936, batch 128, block 16, contexts
@@ -756,7 +815,8 @@ class AdjustLogits:
 
 
 WORKLOADS = {w.name: w for w in (GreedyVerify, StochasticVerify, WindowGather, SummaryUpdate, SoftmaxTempWorkload,
-                                  TargetProbsWorkload, ChainSampling, AdjustLogits, SampleStep, FullRound, HbmCopy)}
+                                  TargetProbsWorkload, ChainSampling, AdjustLogits, SampleStep, Global16Prefill, FullRound,
+                                  HbmCopy)}
 DEFAULT_WORKLOAD = "verify_sample"
 
 

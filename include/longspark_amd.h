@@ -583,6 +583,52 @@ LS_API int ls_summary_scores(const ls_summary_args* args, void* stream);
 LS_API int ls_summary_merge(const ls_summary_args* args, void* stream);
 LS_API int ls_summary_update(const ls_summary_args* args, void* stream);
 
+/* ---- Global16 prefill initialisation ------------------------------------
+ * Replaces Global16Raw256VerifyContext.run_prefill_global_attention
+ * (SRT/speculative/global16_raw256.py:668-784) as driven by
+ * TargetClient._prefill_summaries (src/longspark/engine/target.py:230-253):
+ * one non-causal attention of the summary query rows over each request's
+ * whole prefix, read through its location table (req_to_token rows,
+ * page size 1), returning the output and the natural-log LSE that seed the
+ * incrementally merged state.  The reference runs FA3 once per selected
+ * layer; here every selected layer goes in one launch, split along the prefix.
+ *   output[l][b][h][s][:] = sum_t softmax_t(score) * V[l][loc(b,t)][h/G]
+ *   lse[l][b][h][s]       = logsumexp_t(score),  t < seq_lens[b]
+ *   score = softcap > 0 ? softcap * tanh(q.k * scale / softcap) : q.k * scale
+ * The attention weights enter the weighted sum of values as 16-bit values of
+ * the key type (FA3 rounds P to the element type before its P.V product;
+ * the row sums use the fp32 weights), and the output is rounded to
+ * round_output's type when that is set (FA3 returns the query dtype).  An
+ * empty prefix gives a zero output and LSE -inf. */
+typedef struct ls_prefill_args {
+  int64_t batch;
+  int32_t layers, q_heads, kv_heads, rows, head_dim;
+  int32_t dtype;                       /* LS_BF16 or LS_F16 (queries, keys, values) */
+  float softmax_scale, softcap;
+  /* queries [L][B][Hq][S][D] (stride 0 over requests for a shared query) */
+  const void* query;
+  int64_t q_stride_l, q_stride_b, q_stride_h, q_stride_s;
+  ls_kv_rows keys, values;             /* located rows (located = 1) */
+  /* location table [B][>= max_len] (req_to_token rows), int32 or int64 */
+  const void* page_table;
+  int32_t pt_dtype;
+  int64_t pt_stride_b;
+  int64_t max_len;                     /* table columns; every seq_lens[b] <= max_len */
+  const int32_t* seq_lens;             /* [B] */
+  /* output [L][B][Hq][S][D] and LSE [L][B][Hq][S] fp32 (element strides) */
+  float* output;
+  int64_t o_stride_l, o_stride_b, o_stride_h, o_stride_s;
+  float* lse;
+  int64_t l_stride_l, l_stride_b, l_stride_h, l_stride_s;
+  int32_t round_output;                /* LS_F32 (no rounding), LS_BF16 or LS_F16 */
+  int32_t chunk;                       /* prefix tokens per workgroup, a multiple of 64; 0 = from the sizes */
+} ls_prefill_args;
+
+/* Scratch bytes ls_global16_prefill needs for these arguments (0 when the
+ * prefix is not split). */
+LS_API int ls_global16_prefill_workspace(const ls_prefill_args* args, int64_t* scratch_bytes);
+LS_API int ls_global16_prefill(const ls_prefill_args* args, void* scratch, int64_t scratch_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -107,6 +107,20 @@ class SummaryArgs(ctypes.Structure):
     ]
 
 
+class PrefillArgs(ctypes.Structure):
+    """Mirror of ``ls_prefill_args``."""
+    _fields_ = [
+        ("batch", I64), ("layers", I32), ("q_heads", I32), ("kv_heads", I32), ("rows", I32), ("head_dim", I32),
+        ("dtype", I32), ("softmax_scale", F32), ("softcap", F32),
+        ("query", P), ("q_stride_l", I64), ("q_stride_b", I64), ("q_stride_h", I64), ("q_stride_s", I64),
+        ("keys", KvRows), ("values", KvRows),
+        ("page_table", P), ("pt_dtype", I32), ("pt_stride_b", I64), ("max_len", I64), ("seq_lens", P),
+        ("output", P), ("o_stride_l", I64), ("o_stride_b", I64), ("o_stride_h", I64), ("o_stride_s", I64),
+        ("lse", P), ("l_stride_l", I64), ("l_stride_b", I64), ("l_stride_h", I64), ("l_stride_s", I64),
+        ("round_output", I32), ("chunk", I32),
+    ]
+
+
 # name -> (restype, argtypes).  Kept in the order of include/longspark_amd.h.
 _SIGNATURES = {
     "ls_last_error": (c_char_p, []),
@@ -139,6 +153,8 @@ _SIGNATURES = {
     "ls_summary_scores": (I32, [ctypes.POINTER(SummaryArgs), P]),
     "ls_summary_merge": (I32, [ctypes.POINTER(SummaryArgs), P]),
     "ls_summary_update": (I32, [ctypes.POINTER(SummaryArgs), P]),
+    "ls_global16_prefill_workspace": (I32, [ctypes.POINTER(PrefillArgs), P]),
+    "ls_global16_prefill": (I32, [ctypes.POINTER(PrefillArgs), P, I64, P]),
 }
 
 for _name, (_res, _args) in _SIGNATURES.items():

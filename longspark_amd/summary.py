@@ -237,3 +237,152 @@ def summary_update(*, query: torch.Tensor, key_cache: Layers, value_cache: Layer
     a.state_slots = _lib.ptr(state_slots)
     _locations(a, accepted_cache_locs, accept_lens, accept_offsets, batch, width, what)
     _lib.call("ls_summary_update", ctypes.byref(a), _lib.stream_of(dev))
+
+
+def prefill_global_attention(*, query: torch.Tensor, key_cache: Layers, value_cache: Layers,
+                             page_table: torch.Tensor, cache_seqlens: torch.Tensor, softmax_scale: float,
+                             softcap: float = 0.0, output: Optional[torch.Tensor] = None,
+                             lse: Optional[torch.Tensor] = None, round_output: bool = True, chunk: int = 0):
+    """Prefill summary state of every selected layer in one launch.
+
+    The state ``TargetClient._prefill_summaries`` stacks (src/longspark/engine/
+    target.py:230-253) from one ``run_prefill_global_attention`` per layer
+    (SRT/speculative/global16_raw256.py:668-784): non-causal attention of the
+    summary query rows over each request's whole prefix, the prefix read
+    through its location-table row (req_to_token, page size 1).
+
+    ``query`` ``[L, Hq, S, D]`` (shared by every request, as target.py:234
+    expands it) or ``[B, L, Hq, S, D]``; ``key_cache`` / ``value_cache``
+    per-layer ``[N, Hkv, D]`` pools (a list, or one ``[L, N, Hkv, D]``
+    tensor); ``page_table`` ``[B, >= max length]`` int32/int64 locations;
+    ``cache_seqlens`` ``[B]`` int32.  Returns ``output`` ``[B, L, Hq, S, D]``
+    and ``lse`` ``[B, L, Hq, S]`` fp32 (natural log; an empty prefix gives a
+    zero output and LSE -inf).  ``round_output`` rounds the output to the
+    query dtype, as FA3 returns it in that dtype before the reference widens
+    it to fp32.  ``chunk`` (a multiple of 64, 0 = from the sizes) is the
+    prefix length one workgroup covers.
+    """
+    what = "prefill_global_attention"
+    dev = _lib.require_cuda(query, page_table, cache_seqlens, output, lse, what=what)
+    ks, vs = _check_layers(key_cache, what, "key_cache"), _check_layers(value_cache, what, "value_cache")
+    if page_table.ndim != 2 or page_table.dtype not in (torch.int32, torch.int64) or page_table.stride(1) != 1:
+        raise ValueError("Global16 prefill page table must be a two-dimensional int32/int64 table "
+                         "with contiguous rows")
+    batch = page_table.shape[0]
+    if cache_seqlens.ndim != 1 or cache_seqlens.shape[0] != batch:
+        raise ValueError("Global16 prefill lengths must match the batch")
+    lens = cache_seqlens if cache_seqlens.dtype == torch.int32 else cache_seqlens.to(torch.int32)
+    lens = lens.contiguous()
+    if query.ndim == 4:
+        layers, q_heads, rows, dim = query.shape
+        qs = (query.stride(0) if query.shape[0] > 1 else 0, 0, query.stride(1), query.stride(2))
+    elif query.ndim == 5:
+        if query.shape[0] != batch:
+            raise ValueError(f"{what}: query batch does not match the page table")
+        layers, q_heads, rows, dim = query.shape[1:]
+        qs = (query.stride(1) if query.shape[1] > 1 else 0, query.stride(0), query.stride(2), query.stride(3))
+    else:
+        raise ValueError(f"{what}: query must be [L, Hq, S, D] or [B, L, Hq, S, D]")
+    if query.stride(-1) != 1 or query.dtype not in _QDTYPES:
+        raise ValueError(f"{what}: query must be bf16/fp16 with a contiguous head dimension")
+    if len(ks) != layers or len(vs) != layers:
+        raise ValueError(f"{what}: one key and value pool per layer is required")
+    kv_heads = ks[0].shape[1]
+    if ks[0].shape[2] != dim or vs[0].shape[1:] != ks[0].shape[1:] or ks[0].dtype != query.dtype \
+            or vs[0].dtype != query.dtype:
+        raise ValueError(f"{what}: key/value pools do not match the query geometry")
+    if q_heads % kv_heads:
+        raise ValueError(f"{what}: query heads must be divisible by KV heads")
+    if output is None:
+        output = torch.empty(batch, layers, q_heads, rows, dim, dtype=torch.float32, device=dev)
+    if lse is None:
+        lse = torch.empty(batch, layers, q_heads, rows, dtype=torch.float32, device=dev)
+    if output.shape != (batch, layers, q_heads, rows, dim) or output.dtype != torch.float32 \
+            or output.stride(-1) != 1:
+        raise ValueError(f"{what}: output must be fp32 [B, L, Hq, S, D] with a contiguous head dimension")
+    if lse.shape != (batch, layers, q_heads, rows) or lse.dtype != torch.float32:
+        raise ValueError(f"{what}: lse must be fp32 [B, L, Hq, S]")
+    a = _lib.PrefillArgs()
+    a.batch, a.layers, a.q_heads, a.kv_heads, a.rows, a.head_dim = batch, layers, q_heads, kv_heads, rows, dim
+    a.dtype = _lib.dtype_code(query)
+    a.softmax_scale, a.softcap = float(softmax_scale), float(softcap or 0.0)
+    a.query = query.data_ptr()
+    a.q_stride_l, a.q_stride_b, a.q_stride_h, a.q_stride_s = qs
+    a.keys = _rows(layers=layer_pointers.get(key_cache, dev), stride_loc=ks[0].stride(0), stride_h=ks[0].stride(1),
+                   located=True)
+    a.values = _rows(layers=layer_pointers.get(value_cache, dev), stride_loc=vs[0].stride(0),
+                     stride_h=vs[0].stride(1), located=True)
+    a.page_table, a.pt_dtype = page_table.data_ptr(), _lib.dtype_code(page_table)
+    a.pt_stride_b, a.max_len = page_table.stride(0), page_table.shape[1]
+    a.seq_lens = lens.data_ptr()
+    a.output = output.data_ptr()
+    a.o_stride_l, a.o_stride_b, a.o_stride_h, a.o_stride_s = output.stride(1), output.stride(0), \
+        output.stride(2), output.stride(3)
+    a.lse = lse.data_ptr()
+    a.l_stride_l, a.l_stride_b, a.l_stride_h, a.l_stride_s = lse.stride(1), lse.stride(0), lse.stride(2), \
+        lse.stride(3)
+    a.round_output = _lib.dtype_code(query) if round_output else _lib.LS_F32
+    a.chunk = int(chunk)
+    need = ctypes.c_int64(0)
+    _lib.call("ls_global16_prefill_workspace", ctypes.byref(a), ctypes.byref(need))
+    if batch == 0:
+        return output, lse
+    scratch = torch.empty(max(int(need.value), 16) // 4, dtype=torch.float32, device=dev) if need.value else None
+    _lib.call("ls_global16_prefill", ctypes.byref(a), _lib.ptr(scratch), int(need.value), _lib.stream_of(dev))
+    return output, lse
+
+
+def run_prefill_global_attention(self, *, layer_id: int, layer, key_cache: torch.Tensor, value_cache: torch.Tensor,
+                                 page_table: torch.Tensor, cache_seqlens: torch.Tensor, flash_attn_with_kvcache=None,
+                                 softmax_scale: float, softcap: float, k_descale=None, v_descale=None,
+                                 num_splits: int = 0, extra_kwargs: Optional[dict] = None) -> None:
+    """Method body for ``Global16Raw256VerifyContext.run_prefill_global_attention``
+    (SRT/speculative/global16_raw256.py:668-784): same checks and messages,
+    same state record; the attention runs on ``prefill_global_attention``
+    instead of the ``flash_attn_with_kvcache`` callable (which is ignored, as
+    are ``num_splits`` and ``extra_kwargs``).  ``key_cache`` / ``value_cache``
+    are the layer's ``[N, 1, Hkv, D]`` (page size 1) or ``[N, Hkv, D]`` pools.
+    """
+    import sys
+
+    layer_id = int(layer_id)
+    if self.incremental_from_prior or self.committed:
+        raise RuntimeError("Global16 prefill scan requires a fresh context")
+    if not self.applies_to(layer_id):
+        raise ValueError(f"layer {layer_id} is not selected for Global16")
+    if layer_id in self.layer_states:
+        raise RuntimeError("Global16 prefill state may be initialized only once")
+    if page_table.ndim != 2:
+        raise ValueError("Global16 prefill page table must be two-dimensional")
+    if k_descale is not None or v_descale is not None:
+        raise NotImplementedError("Global16 prefill: scaled (fp8) key/value caches are not supported")
+    cache_seqlens = cache_seqlens.to(device=self.global_queries.device, dtype=torch.int32)
+    if cache_seqlens.ndim != 1 or cache_seqlens.shape[0] != page_table.shape[0]:
+        raise ValueError("Global16 prefill lengths must match the batch")
+    source_rows = self.source_batch_rows.to(device=page_table.device)
+    page_table = page_table.index_select(0, source_rows)
+    cache_seqlens = cache_seqlens.index_select(0, source_rows)
+
+    def pool(t: torch.Tensor) -> torch.Tensor:
+        if t.ndim == 4:
+            if t.shape[1] != 1:
+                raise ValueError("Global16 prefill: only page size 1 caches are supported")
+            t = t[:, 0]
+        return t
+
+    query = self._query_for_layer(layer_id)                      # [B, Hq, S, D]
+    output, lse = prefill_global_attention(query=query[:, None], key_cache=[pool(key_cache)],
+                                           value_cache=[pool(value_cache)], page_table=page_table,
+                                           cache_seqlens=cache_seqlens, softmax_scale=softmax_scale,
+                                           softcap=softcap)
+    mod = sys.modules[type(self).__module__]
+    self.layer_states[layer_id] = mod.Global16Raw256LayerState(query=query, output=output[:, 0],
+                                                               logsumexp=lse[:, 0])
+    self.layer_objects[layer_id] = layer
+    prefix_rows = int(self.confirmed_prefix_lens.sum().item()) if self.collect_fixed_cost_audit else 0
+    self.joint_evidence[layer_id] = mod.Global16Raw256FAEvidence(
+        layer_id=layer_id, fa3_invocations=1, key_cache_storage_ptr=key_cache.untyped_storage().data_ptr(),
+        value_cache_storage_ptr=value_cache.untyped_storage().data_ptr(), target_query_rows=0,
+        global_query_rows=self.batch_size * query.shape[2], duplicated_page_table_rows=0,
+        request_layer_base_inits=self.batch_size, prefix_rows=prefix_rows,
+        query_key_pairs=prefix_rows * query.shape[2])

@@ -7,7 +7,10 @@ summary slots S, new rows W, query heads Hq and KV heads Hkv:
   * full-prefix state (fp64 ground truth) -- the definition that
     vendor/specforge/modeling/draft/global16_raw256.py:829-869
     (``global_state_from_full_prefix``) computes and :871-915
-    (``commit_accepted_delta``) must reproduce incrementally.
+    (``commit_accepted_delta``) must reproduce incrementally;
+  * prefill initialisation -- SRT/speculative/global16_raw256.py:668-784
+    (one FA3 ``flash_attn_with_kvcache`` per layer, non-causal, over each
+    request's location-table row): that full-prefix state per request.
 ``SRT`` abbreviates ``vendor/sglang/python/sglang/srt``.  GQA maps query head
 h to KV head ``h // (Hq // Hkv)`` (consecutive groups share a KV head).
 """
@@ -59,12 +62,13 @@ def merge_accepted_positions(state_output, state_lse, position_scores_, accepted
     return state_output.float() * prior_weight[..., None] + delta_out, merged_lse
 
 
-def full_prefix_state(global_query, keys, values, softmax_scale: float, dtype=torch.float64):
+def full_prefix_state(global_query, keys, values, softmax_scale: float, dtype=torch.float64, softcap: float = 0.0):
     """Normalised attention output and LSE of every query row over a whole prefix.
 
     ``keys``/``values`` are ``[B, T, Hkv, D]``.  This is the quantity the
     incremental merge maintains: after folding every prefix row, the state must
-    equal ``softmax(scale * q k^T) v`` with ``lse = logsumexp(scale * q k^T)``.
+    equal ``softmax(scale * q k^T) v`` with ``lse = logsumexp(scale * q k^T)``
+    (scores through ``softcap * tanh(s / softcap)`` when softcap > 0).
     """
     batch, hq, rows, dim = global_query.shape
     hkv = keys.shape[2]
@@ -73,6 +77,8 @@ def full_prefix_state(global_query, keys, values, softmax_scale: float, dtype=to
     k = keys.to(dtype).permute(0, 2, 1, 3)
     v = values.to(dtype).permute(0, 2, 1, 3)
     s = torch.einsum("bhgrd,bhtd->bhgrt", q, k) * softmax_scale
+    if softcap > 0:
+        s = torch.tanh(s / softcap) * softcap
     lse = torch.logsumexp(s, dim=-1)
     out = torch.einsum("bhgrt,bhtd->bhgrd", torch.softmax(s, dim=-1), v)
     return out.reshape(batch, hq, rows, dim), lse.reshape(batch, hq, rows)
@@ -89,4 +95,33 @@ def summary_update(state_output, state_lse, global_query, new_keys, new_values, 
     o, l = merge_accepted_positions(out[slots], lse[slots], scores, new_values, accept_lens)
     out[slots] = o
     lse[slots] = l
+    return out, lse
+
+
+def prefill_global_attention(global_query, key_cache, value_cache, page_table, seq_lens, softmax_scale: float,
+                             softcap: float = 0.0, dtype=torch.float64):
+    """One layer's prefill state: ``[B, Hq, S, D]`` output and ``[B, Hq, S]`` LSE.
+
+    global16_raw256.py:709-760: request b attends over the pool rows
+    ``page_table[b, :seq_lens[b]]`` of ``key_cache`` / ``value_cache``
+    (``[N, Hkv, D]``, page size 1), non-causal, every position visible.
+    ``global_query`` is ``[B, Hq, S, D]`` or ``[Hq, S, D]`` (shared).  An
+    empty prefix gives a zero output and LSE -inf.  Exact (fp64) values: the
+    reference's FA3 rounds the weights and its output to bf16, which the
+    comparison tolerance covers.
+    """
+    batch = page_table.shape[0]
+    if global_query.ndim == 3:
+        global_query = global_query[None].expand(batch, -1, -1, -1)
+    _, hq, rows, dim = global_query.shape
+    out = torch.zeros(batch, hq, rows, dim, dtype=dtype)
+    lse = torch.full((batch, hq, rows), float("-inf"), dtype=dtype)
+    for b in range(batch):
+        n = int(seq_lens[b])
+        if n <= 0:
+            continue
+        locs = page_table[b, :n].long()
+        o, l = full_prefix_state(global_query[b:b + 1], key_cache[locs][None], value_cache[locs][None],
+                                 softmax_scale, dtype=dtype, softcap=softcap)
+        out[b], lse[b] = o[0], l[0]
     return out, lse

@@ -114,3 +114,79 @@ def test_rows_past_accept_len_do_not_matter():
     v2[1, 5:] = 1e30
     b = osm.merge_accepted_positions(out0, lse0, sc2, v2, lens)
     assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+
+
+def _pool(g, n, hkv, dim, dtype=torch.bfloat16):
+    return torch.randn(n, hkv, dim, generator=g).to(dtype), torch.randn(n, hkv, dim, generator=g).to(dtype)
+
+
+@pytest.mark.parametrize("hq,hkv", [(8, 2), (5, 1)])
+def test_prefill_equals_empty_prior_folding(hq, hkv):
+    """The prefill state through a permuted location table equals folding the
+    prefix from an empty state (lse -inf) with the incremental merge."""
+    g = torch.Generator().manual_seed(40 + hq)
+    batch, rows, dim, n = 3, 4, 16, 200
+    scale = dim ** -0.5
+    q = torch.randn(batch, hq, rows, dim, generator=g).to(torch.bfloat16)
+    kc, vc = _pool(g, n, hkv, dim)
+    table = torch.randperm(n, generator=g)[: batch * 40].view(batch, 40).to(torch.int32)
+    lens = torch.tensor([40, 17, 1], dtype=torch.int32)
+    out, lse = osm.prefill_global_attention(q, kc, vc, table, lens, scale)
+    for b in range(batch):
+        o = torch.zeros(1, hq, rows, dim)
+        l = torch.full((1, hq, rows), -math.inf)
+        width = 8
+        for p0 in range(0, int(lens[b]), width):
+            m = min(width, int(lens[b]) - p0)
+            locs = torch.full((width,), int(table[b, p0]), dtype=torch.long)
+            locs[:m] = table[b, p0:p0 + m].long()
+            sc = osm.position_scores(q[b:b + 1], kc[locs][None], scale)
+            o, l = osm.merge_accepted_positions(o, l, sc, vc[locs][None], torch.tensor([m], dtype=torch.int32))
+        assert torch.allclose(out[b].float(), o[0], rtol=1e-5, atol=1e-5)
+        assert torch.allclose(lse[b].float(), l[0], rtol=1e-5, atol=1e-5)
+
+
+def test_prefill_matches_library_attention():
+    """Output against torch's scaled_dot_product_attention (fp64, KV heads
+    repeated over consecutive query-head groups)."""
+    g = torch.Generator().manual_seed(44)
+    batch, hq, hkv, rows, dim, n = 2, 6, 2, 5, 32, 90
+    scale = 0.3
+    q = torch.randn(hq, rows, dim, generator=g).to(torch.bfloat16)   # shared by the requests
+    kc, vc = _pool(g, n, hkv, dim)
+    table = torch.stack([torch.randperm(n, generator=g)[:60] for _ in range(batch)]).to(torch.int64)
+    lens = torch.tensor([60, 23], dtype=torch.int32)
+    out, _ = osm.prefill_global_attention(q, kc, vc, table, lens, scale)
+    for b in range(batch):
+        locs = table[b, : int(lens[b])]
+        k = kc[locs].double().permute(1, 0, 2).repeat_interleave(hq // hkv, dim=0)
+        v = vc[locs].double().permute(1, 0, 2).repeat_interleave(hq // hkv, dim=0)
+        ref = torch.nn.functional.scaled_dot_product_attention(q.double(), k, v, scale=scale)
+        assert torch.allclose(out[b], ref, rtol=1e-10, atol=1e-12)
+
+
+def test_prefill_closed_forms():
+    g = torch.Generator().manual_seed(45)
+    hq, hkv, rows, dim, scale, cap = 4, 2, 3, 8, 0.5, 2.0
+    q = torch.randn(1, hq, rows, dim, generator=g).to(torch.bfloat16)
+    kc, vc = _pool(g, 10, hkv, dim)
+    # one prefix token: output = its value row, lse = its (capped) score
+    table = torch.tensor([[7, 0, 0]], dtype=torch.int32)
+    out, lse = osm.prefill_global_attention(q, kc, vc, table, torch.tensor([1]), scale, softcap=cap)
+    for h in range(hq):
+        kv = h // (hq // hkv)
+        assert torch.allclose(out[0, h], vc[7, kv].double()[None].expand(rows, -1))
+        s = (q[0, h].double() @ kc[7, kv].double()) * scale
+        assert torch.allclose(lse[0, h], cap * torch.tanh(s / cap))
+    # n copies of one key: output = mean of the values, lse = s + ln n
+    kc[:, :] = kc[3]
+    table = torch.tensor([[0, 1, 2, 3, 4, 5]], dtype=torch.int32)
+    out, lse = osm.prefill_global_attention(q, kc, vc, table, torch.tensor([6]), scale)
+    for h in range(hq):
+        kv = h // (hq // hkv)
+        assert torch.allclose(out[0, h], vc[:6, kv].double().mean(0)[None].expand(rows, -1))
+        s = (q[0, h].double() @ kc[3, kv].double()) * scale
+        assert torch.allclose(lse[0, h], s + math.log(6))
+    # empty prefix
+    out, lse = osm.prefill_global_attention(q, kc, vc, table, torch.tensor([0]), scale)
+    assert bool((out == 0).all()) and bool(torch.isneginf(lse).all())
