@@ -17,10 +17,10 @@
 //
 // Per 32-token step (64 for head_dim 64):
 //   staging  K rows -> LDS as they are ([token][d]); V rows -> LDS transposed
-//            ([d][token]) so that a lane's A operand of the P.V product is
-//            two 8-byte reads.  The next step's rows are loaded into
-//            registers while this step computes, and the step after next's
-//            locations are loaded too.
+//            ([d][token], two tokens per 4-byte write) so that a lane's A
+//            operand of the P.V product is two 8-byte reads.  The rows of the
+//            next two steps are in flight in registers while a step computes.
+//            The tile's query rows sit in LDS for the whole split.
 //   scores   S^T[16 tok x 16 rows] = K[16 x D] . Q^T[D x 16]   (16x16x32 MFMA);
 //            the lane holding row c16 gets tokens 4*g16 + i of each tile.
 //   softmax  running maximum in the base-2 domain (s * log2 e), weights
@@ -48,7 +48,7 @@ struct PrefillShape {
   static constexpr int kVP = kBlk + 4;                // 16-bit elements per LDS transposed value row
   static constexpr int kChunks = D / 8;               // 16-byte vectors per row
   static constexpr int kKVecs = kBlk * kChunks;       // key vectors per step
-  static constexpr int kVUnits = (kBlk / 4) * kChunks;  // value units (4 tokens x 8 d) per step
+  static constexpr int kVUnits = (kBlk / 2) * kChunks;  // value units (2 tokens x 8 d) per step
   static constexpr int kKR = (kKVecs + kMinThreads - 1) / kMinThreads;   // per-thread key vectors
   static constexpr int kVR = (kVUnits + kMinThreads - 1) / kMinThreads;  // per-thread value units
   static constexpr int kNT = kBlk / 16;               // 16-token score tiles per step
@@ -84,11 +84,12 @@ __device__ __forceinline__ uint32_t pack_weights<F16>(float lo, float hi) {
   return static_cast<uint32_t>(__half_as_ushort(a)) | (static_cast<uint32_t>(__half_as_ushort(b)) << 16);
 }
 
-// Location of prefix token t of request b (pool rows are below 2^31).
+// Location of prefix token t of request b (pool rows are below 2^31): the
+// low 32-bit word of an int64 entry, read without a branch (a branch around
+// a load makes the compiler wait for every load issued before it).
 __device__ __forceinline__ int table_loc(const ls_prefill_args& a, int64_t b, int64_t t) {
-  const int64_t i = b * a.pt_stride_b + t;
-  return a.pt_dtype == LS_I64 ? static_cast<int>(static_cast<const int64_t*>(a.page_table)[i])
-                              : static_cast<const int32_t*>(a.page_table)[i];
+  const int shift = a.pt_dtype == LS_I64 ? 1 : 0;
+  return static_cast<const int32_t*>(a.page_table)[(b * a.pt_stride_b + t) << shift];
 }
 
 __device__ __forceinline__ int clamp_len(const ls_prefill_args& a, int64_t b) {
@@ -102,7 +103,7 @@ __device__ __forceinline__ uint32_t half_of(const uint4& v, int e) {
   return (e & 1) ? (w >> 16) : (w & 0xffffu);
 }
 
-template <int D, typename Tag>
+template <int D, typename Tag, bool kCap>
 __device__ __forceinline__ void prefill_body(const ls_prefill_args& a, const PrefillGeom& g, float* __restrict__ part_o,
                                              float* __restrict__ part_mz) {
   using Sh = PrefillShape<D>;
@@ -112,16 +113,18 @@ __device__ __forceinline__ void prefill_body(const ls_prefill_args& a, const Pre
   uint16_t* vls = kls + kBlk * Sh::kKP;
 
   // XCD-aware unit: blocks go round-robin over 8 XCDs; each XCD takes a
-  // contiguous range of units (consecutive splits of one request and head).
+  // contiguous range of units.  The KV head varies fastest, so the
+  // workgroups that read the 256-byte head slices of the same 2 KiB token
+  // rows run side by side on one XCD and move through the prefix together.
   const unsigned nb = gridDim.x, bi = blockIdx.x;
   const unsigned per = nb / 8, rem = nb % 8, xcd = bi % 8;
   int64_t u = static_cast<int64_t>(xcd) * per + min(xcd, rem) + bi / 8;
-  const int split = static_cast<int>(u % g.nsplit);
-  u /= g.nsplit;
-  const int tile = static_cast<int>(u % g.tiles);
-  u /= g.tiles;
   const int kvh = static_cast<int>(u % a.kv_heads);
   u /= a.kv_heads;
+  const int tile = static_cast<int>(u % g.tiles);
+  u /= g.tiles;
+  const int split = static_cast<int>(u % g.nsplit);
+  u /= g.nsplit;
   const int layer = static_cast<int>(u % a.layers);
   const int64_t b = u / a.layers;
 
@@ -156,114 +159,112 @@ __device__ __forceinline__ void prefill_body(const ls_prefill_args& a, const Pre
   const char* kbase = layer_base(a.keys, layer) + kvh * a.keys.stride_h * 2;
   const char* vbase = layer_base(a.values, layer) + kvh * a.values.stride_h * 2;
 
-  // Query row as the B operand of S^T: depth kb*32 + 8*g16 .. +7.
-  uint4 qb[Sh::kKB];
-  {
+  // Query rows of this tile -> LDS (pitch kKP); each wave reads its rows as
+  // the B operand of S^T (depth kb*32 + 8*g16 .. +7).
+  uint16_t* qls = vls + D * Sh::kVP;
+  const int tile_rows = min(nrows - tile * kMaxRowsPerTile, kMaxRowsPerTile);
+  for (int j = tid; j < tile_rows * Sh::kChunks; j += nthr) {
+    const int rl = j / Sh::kChunks, c = j % Sh::kChunks;
+    const int r2 = tile * kMaxRowsPerTile + rl;
+    const int h2 = kvh * groups + r2 / a.rows, s2 = r2 % a.rows;
     const char* q = static_cast<const char*>(a.query) +
-                    (layer * a.q_stride_l + b * a.q_stride_b + head * a.q_stride_h + srow * a.q_stride_s) * 2;
-#pragma unroll
-    for (int kb = 0; kb < Sh::kKB; ++kb) qb[kb] = load16(q + (kb * 32 + g16 * 8) * 2);
+                    (layer * a.q_stride_l + b * a.q_stride_b + h2 * a.q_stride_h + s2 * a.q_stride_s) * 2;
+    *reinterpret_cast<uint4*>(qls + rl * Sh::kKP + c * 8) = load16(q + c * 16);
   }
+  const uint16_t* qrow = qls + min(wave * 16 + c16, tile_rows - 1) * Sh::kKP + g16 * 8;
 
   // Staging assignment: key vector j = i*nthr + tid (token j / kChunks,
-  // chunk j % kChunks); value unit v = i*nthr + tid (tokens 4*(v % (kBlk/4))
-  // .. +3, chunk v / (kBlk/4)).
-  int kloc[Sh::kKR], vloc[Sh::kVR][4];
-  uint4 kreg[Sh::kKR], vreg[Sh::kVR][4];
-  auto load_locs = [&](int tb) __attribute__((always_inline)) {
+  // chunk j % kChunks); value unit v = i*nthr + tid (tokens 2*(v % (kBlk/2))
+  // and the next, chunk v / (kBlk/2)).  Loads are issued with no branch
+  // around them: indices past the step's work are clamped and tokens past
+  // the prefix read the last prefix token (those rows get weight 0, so their
+  // finite contents are unused).  A load behind a branch makes the compiler
+  // wait for every earlier load before issuing it.
+  struct Locs { int k[Sh::kKR], v[Sh::kVR][2]; };
+  struct Rows { uint4 k[Sh::kKR], v[Sh::kVR][2]; };
+  auto load_locs = [&](Locs& L, int tb) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < Sh::kKR; ++i) {
-      const int j = i * nthr + tid;
-      const int t = min(tb + (j < Sh::kKVecs ? j / Sh::kChunks : 0), t_end - 1);
-      kloc[i] = table_loc(a, b, t);
+      const int j = min(i * nthr + tid, Sh::kKVecs - 1);
+      L.k[i] = table_loc(a, b, min(tb + j / Sh::kChunks, t_end - 1));
     }
 #pragma unroll
     for (int i = 0; i < Sh::kVR; ++i) {
-      const int v = i * nthr + tid;
-      const int q4 = v < Sh::kVUnits ? v % (kBlk / 4) : 0;
+      const int v = min(i * nthr + tid, Sh::kVUnits - 1);
+      const int p2 = v % (kBlk / 2);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) vloc[i][e] = table_loc(a, b, min(tb + 4 * q4 + e, t_end - 1));
+      for (int e = 0; e < 2; ++e) L.v[i][e] = table_loc(a, b, min(tb + 2 * p2 + e, t_end - 1));
     }
   };
-  auto load_rows = [&](int tb) __attribute__((always_inline)) {
+  auto load_rows = [&](Rows& R, const Locs& L) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < Sh::kKR; ++i) {
-      const int j = i * nthr + tid;
-      kreg[i] = make_uint4(0, 0, 0, 0);
-      if (j < Sh::kKVecs && tb + j / Sh::kChunks < t_end)
-        kreg[i] = load16_global(kbase + (static_cast<int64_t>(kloc[i]) * a.keys.stride_loc + (j % Sh::kChunks) * 8) * 2);
+      const int j = min(i * nthr + tid, Sh::kKVecs - 1);
+      R.k[i] = load16_global(kbase + (static_cast<int64_t>(L.k[i]) * a.keys.stride_loc + (j % Sh::kChunks) * 8) * 2);
     }
 #pragma unroll
     for (int i = 0; i < Sh::kVR; ++i) {
-      const int v = i * nthr + tid;
-      const int q4 = v % (kBlk / 4), c = v / (kBlk / 4);
+      const int v = min(i * nthr + tid, Sh::kVUnits - 1);
+      const int c = v / (kBlk / 2);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        vreg[i][e] = make_uint4(0, 0, 0, 0);
-        if (v < Sh::kVUnits && tb + 4 * q4 + e < t_end)
-          vreg[i][e] = load16_global(vbase + (static_cast<int64_t>(vloc[i][e]) * a.values.stride_loc + c * 8) * 2);
-      }
+      for (int e = 0; e < 2; ++e)
+        R.v[i][e] = load16_global(vbase + (static_cast<int64_t>(L.v[i][e]) * a.values.stride_loc + c * 8) * 2);
     }
   };
-  auto store_rows = [&]() __attribute__((always_inline)) {
+  auto store_rows = [&](const Rows& R) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < Sh::kKR; ++i) {
       const int j = i * nthr + tid;
       if (j < Sh::kKVecs)
-        *reinterpret_cast<uint4*>(kls + (j / Sh::kChunks) * Sh::kKP + (j % Sh::kChunks) * 8) = kreg[i];
+        *reinterpret_cast<uint4*>(kls + (j / Sh::kChunks) * Sh::kKP + (j % Sh::kChunks) * 8) = R.k[i];
     }
 #pragma unroll
     for (int i = 0; i < Sh::kVR; ++i) {
       const int v = i * nthr + tid;
       if (v < Sh::kVUnits) {
-        const int q4 = v % (kBlk / 4), c = v / (kBlk / 4);
+        const int p2 = v % (kBlk / 2), c = v / (kBlk / 2);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          uint2 w;
-          w.x = half_of(vreg[i][0], e) | (half_of(vreg[i][1], e) << 16);
-          w.y = half_of(vreg[i][2], e) | (half_of(vreg[i][3], e) << 16);
-          *reinterpret_cast<uint2*>(vls + (c * 8 + e) * Sh::kVP + 4 * q4) = w;
-        }
+        for (int e = 0; e < 8; ++e)
+          *reinterpret_cast<uint32_t*>(vls + (c * 8 + e) * Sh::kVP + 2 * p2) =
+              half_of(R.v[i][0], e) | (half_of(R.v[i][1], e) << 16);
       }
     }
   };
 
-  const float qk_scale = a.softcap > 0.f ? a.softmax_scale : a.softmax_scale * kLog2e;
+  const float qk_scale = kCap ? a.softmax_scale : a.softmax_scale * kLog2e;
   f32x4_t o[Sh::kDB];
 #pragma unroll
   for (int db = 0; db < Sh::kDB; ++db) o[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   float m = -__builtin_inff(), z = 0.f;
 
-  load_locs(t0);
-  load_rows(t0);
-  if (nblk > 1) load_locs(t0 + kBlk);
-  for (int blk = 0; blk < nblk; ++blk) {
-    const int tb = t0 + blk * kBlk;
-    lds_barrier();  // the previous step's reads of the staged rows are done
-    store_rows();
-    lds_barrier();
-    if (blk + 1 < nblk) {
-      load_rows(tb + kBlk);
-      if (blk + 2 < nblk) load_locs(tb + 2 * kBlk);
-    }
-    if (!wave_rows) continue;
-
+  auto compute = [&](int tb) __attribute__((always_inline)) {
     // scores of this lane's row: sc[nt][i] = s(row c16, token tb + nt*16 + 4*g16 + i), base 2
     f32x4_t sc[Sh::kNT];
 #pragma unroll
-    for (int nt = 0; nt < Sh::kNT; ++nt) {
-      f32x4_t t = {0.f, 0.f, 0.f, 0.f};
+    for (int nt = 0; nt < Sh::kNT; ++nt) sc[nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int kb = 0; kb < Sh::kKB; ++kb) {
+    for (int kb = 0; kb < Sh::kKB; ++kb) {
+      const uint4 qv = *reinterpret_cast<const uint4*>(qrow + kb * 32);
+#pragma unroll
+      for (int nt = 0; nt < Sh::kNT; ++nt) {
         const uint4 kv = *reinterpret_cast<const uint4*>(kls + (nt * 16 + c16) * Sh::kKP + kb * 32 + g16 * 8);
-        t = Mma<Tag>::run(kv, qb[kb], t);
+        sc[nt] = Mma<Tag>::run(kv, qv, sc[nt]);
       }
+    }
+#pragma unroll
+    for (int nt = 0; nt < Sh::kNT; ++nt)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        float s = t[i] * qk_scale;
-        if (a.softcap > 0.f) s = tanhf(s / a.softcap) * a.softcap * kLog2e;
-        sc[nt][i] = tb + nt * 16 + 4 * g16 + i < t_end ? s : -__builtin_inff();
+        float s = sc[nt][i] * qk_scale;
+        if constexpr (kCap) s = tanhf(s / a.softcap) * a.softcap * kLog2e;
+        sc[nt][i] = s;
       }
+    if (tb + kBlk > t_end) {  // uniform: the step runs past the prefix
+#pragma unroll
+      for (int nt = 0; nt < Sh::kNT; ++nt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (tb + nt * 16 + 4 * g16 + i >= t_end) sc[nt][i] = -__builtin_inff();
     }
     float bm = -__builtin_inff();
 #pragma unroll
@@ -272,19 +273,23 @@ __device__ __forceinline__ void prefill_body(const ls_prefill_args& a, const Pre
       for (int i = 0; i < 4; ++i) bm = fmaxf(bm, sc[nt][i]);
     bm = fmaxf(bm, __shfl_xor(bm, 16, kWave));
     bm = fmaxf(bm, __shfl_xor(bm, 32, kWave));
-    const float mn = fmaxf(m, bm);  // finite: every step holds at least one prefix token
-    const float alpha = __builtin_amdgcn_exp2f(m - mn);
+    // finite after the first step (it holds at least one prefix token); a
+    // padding step past the prefix leaves m unchanged and adds nothing
+    const float mn = fmaxf(m, bm);
+    const float alpha = __builtin_amdgcn_exp2f(m - mn);  // exactly 1 where the maximum held
     m = mn;
-    z *= alpha;
+    if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {  // uniform: rescale only when a maximum rose
+      z *= alpha;
 #pragma unroll
-    for (int db = 0; db < Sh::kDB; ++db) o[db] *= alpha;
+      for (int db = 0; db < Sh::kDB; ++db) o[db] *= alpha;
+    }
 #pragma unroll
     for (int nt = 0; nt < Sh::kNT; ++nt)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float p = __builtin_amdgcn_exp2f(sc[nt][i] - mn);
-        sc[nt][i] = p;
-        z += p;
+        const float pw = __builtin_amdgcn_exp2f(sc[nt][i] - mn);
+        sc[nt][i] = pw;
+        z += pw;
       }
 #pragma unroll
     for (int kb = 0; kb < kBlk / 32; ++kb) {
@@ -301,6 +306,47 @@ __device__ __forceinline__ void prefill_body(const ls_prefill_args& a, const Pre
         o[db] = Mma<Tag>::run(make_uint4(lo.x, lo.y, hi.x, hi.y), pb, o[db]);
       }
     }
+  };
+
+  // Two steps of rows in flight: at step n the rows of step n+1 are loading,
+  // the rows of step n+2 are issued (into the registers step n has just
+  // stored), and the locations of step n+3 are issued before them so that
+  // waiting for those locations later never waits for rows still in flight.
+  // The step count is padded to even (a padding step lies past the prefix:
+  // every weight 0) so that the two register sets alternate without a branch.
+  Locs L0, L1;
+  Rows R0, R1;
+  // (scheduling barriers keep the issue order of the loop body, which the
+  // compiler's wait counts at the loop head assume)
+  load_locs(L0, t0);
+  load_locs(L1, t0 + kBlk);
+  __builtin_amdgcn_sched_barrier(0);
+  load_rows(R0, L0);
+  __builtin_amdgcn_sched_barrier(0);
+  load_locs(L0, t0 + 2 * kBlk);
+  __builtin_amdgcn_sched_barrier(0);
+  load_rows(R1, L1);
+  __builtin_amdgcn_sched_barrier(0);
+  const int nsteps = (nblk + 1) & ~1;
+  for (int n = 0; n < nsteps; n += 2) {
+    const int tb = t0 + n * kBlk;
+    lds_barrier();  // the previous step's reads of the staged rows are done
+    store_rows(R0);
+    lds_barrier();
+    load_locs(L1, tb + 3 * kBlk);
+    __builtin_amdgcn_sched_barrier(0);
+    load_rows(R0, L0);
+    __builtin_amdgcn_sched_barrier(0);
+    if (wave_rows) compute(tb);
+
+    lds_barrier();
+    store_rows(R1);
+    lds_barrier();
+    load_locs(L0, tb + 4 * kBlk);
+    __builtin_amdgcn_sched_barrier(0);
+    load_rows(R1, L1);
+    __builtin_amdgcn_sched_barrier(0);
+    if (wave_rows) compute(tb + kBlk);
   }
   if (!valid) return;
   z += __shfl_xor(z, 16, kWave);
@@ -332,17 +378,18 @@ __device__ __forceinline__ void prefill_body(const ls_prefill_args& a, const Pre
   if (g16 == 0) *reinterpret_cast<float2*>(part_mz + prow * 2) = make_float2(m, z);
 }
 
-// Head dims up to 128 fit four waves per SIMD; 256 keeps two.
-template <int D, typename Tag>
+// Head dims up to 128 fit four waves per SIMD; 256 keeps two.  kCap: scores
+// pass through softcap * tanh(s / softcap).
+template <int D, typename Tag, bool kCap>
 __global__ __launch_bounds__(kMaxThreads) __attribute__((amdgpu_waves_per_eu(4))) void prefill_kernel(
     const ls_prefill_args a, const PrefillGeom g, float* __restrict__ part_o, float* __restrict__ part_mz) {
-  prefill_body<D, Tag>(a, g, part_o, part_mz);
+  prefill_body<D, Tag, kCap>(a, g, part_o, part_mz);
 }
-template <typename Tag>
+template <typename Tag, bool kCap>
 __global__ __launch_bounds__(kMaxThreads) void prefill_kernel_d256(const ls_prefill_args a, const PrefillGeom g,
                                                                     float* __restrict__ part_o,
                                                                     float* __restrict__ part_mz) {
-  prefill_body<256, Tag>(a, g, part_o, part_mz);
+  prefill_body<256, Tag, kCap>(a, g, part_o, part_mz);
 }
 
 // One wave per (request, layer, query row of a KV head): merge the splits
@@ -399,6 +446,35 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(const ls_prefill_a
         ns > 0 ? (mx + log2f(zs)) * kLn2 : -__builtin_inff();
 }
 
+size_t prefill_lds(int d, int nrows) {
+  const int tile_rows = nrows < kMaxRowsPerTile ? nrows : kMaxRowsPerTile;
+  switch (d) {
+    case 64: return PrefillShape<64>::kLds + static_cast<size_t>(tile_rows) * PrefillShape<64>::kKP * 2;
+    case 128: return PrefillShape<128>::kLds + static_cast<size_t>(tile_rows) * PrefillShape<128>::kKP * 2;
+    default: return PrefillShape<256>::kLds + static_cast<size_t>(tile_rows) * PrefillShape<256>::kKP * 2;
+  }
+}
+
+// Workgroups resident on the device at once: CUs x per-CU limit from wave
+// slots (4 waves per SIMD for head_dim <= 128, 2 for 256) and 160 KiB of LDS.
+int64_t resident_slots(int d, int threads, size_t lds) {
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+      cus = n;
+    else
+      cus = 256;
+    (void)hipGetLastError();
+  }
+  const int waves = threads / kWave;
+  const int by_waves = (d == 256 ? 8 : 16) / waves;
+  const int by_lds = static_cast<int>((160 * 1024) / lds);
+  const int per_cu = by_waves < by_lds ? by_waves : by_lds;
+  return static_cast<int64_t>(cus) * (per_cu > 0 ? per_cu : 1);
+}
+
 bool kv_rows_aligned(const ls_kv_rows& r) {
   return r.located && (r.stride_loc * 2) % 16 == 0 && (r.stride_h * 2) % 16 == 0 &&
          (r.layers || ((r.stride_layer * 2) % 16 == 0 && aligned16(r.base)));
@@ -447,8 +523,10 @@ int prefill_geometry(const ls_prefill_args* ap, const char* what, bool launch, P
   const int64_t base = a.batch * a.layers * a.kv_heads * g->tiles;
   int64_t chunk = a.chunk;
   if (chunk == 0) {
-    // about 2048 workgroups (8 per CU), at least 512 prefix tokens each
-    const int64_t want = base > 0 ? (2048 + base - 1) / base : 1;
+    // As many splits as fill the resident workgroup slots once (a partial
+    // second round would leave most CUs idle), at least 512 prefix tokens each.
+    const int64_t slots = resident_slots(a.head_dim, g->threads, prefill_lds(a.head_dim, nrows));
+    const int64_t want = base > 0 && slots > base ? slots / base : 1;
     chunk = (a.max_len + want - 1) / want;
     chunk = (chunk + 63) / 64 * 64;
     if (chunk < 512) chunk = 512;
@@ -465,12 +543,19 @@ int prefill_geometry(const ls_prefill_args* ap, const char* what, bool launch, P
 
 template <int D, typename Tag>
 int launch_prefill(const ls_prefill_args& a, const PrefillGeom& g, float* part_o, float* part_mz, hipStream_t st) {
-  if constexpr (D == 256)
-    prefill_kernel_d256<Tag><<<dim3(static_cast<unsigned>(g.units)), g.threads, PrefillShape<D>::kLds, st>>>(
-        a, g, part_o, part_mz);
-  else
-    prefill_kernel<D, Tag><<<dim3(static_cast<unsigned>(g.units)), g.threads, PrefillShape<D>::kLds, st>>>(
-        a, g, part_o, part_mz);
+  const size_t lds = prefill_lds(D, (a.q_heads / a.kv_heads) * a.rows);
+  const dim3 grid(static_cast<unsigned>(g.units));
+  if constexpr (D == 256) {
+    if (a.softcap > 0.f)
+      prefill_kernel_d256<Tag, true><<<grid, g.threads, lds, st>>>(a, g, part_o, part_mz);
+    else
+      prefill_kernel_d256<Tag, false><<<grid, g.threads, lds, st>>>(a, g, part_o, part_mz);
+  } else {
+    if (a.softcap > 0.f)
+      prefill_kernel<D, Tag, true><<<grid, g.threads, lds, st>>>(a, g, part_o, part_mz);
+    else
+      prefill_kernel<D, Tag, false><<<grid, g.threads, lds, st>>>(a, g, part_o, part_mz);
+  }
   LS_LAUNCH_CHECK();
   if (g.nsplit > 1) {
     const int64_t waves = a.batch * a.layers * a.kv_heads * static_cast<int64_t>((a.q_heads / a.kv_heads) * a.rows);
