@@ -45,6 +45,8 @@ TRAFFIC = {
     "chain_kernel": (158_497_097, "profiles/chain_kernel_chain_sampling_B128_K16_V151936.md"),
     "request_bias_kernel": (1_403_662_037, "profiles/request_bias_kernel_adjust_logits_B128_K16_V151936.md"),
     "sample_step_kernel": (156_653_721, "profiles/sample_step_kernel_B128_V151936.md"),
+    "prefill_kernel + prefill_combine_kernel": (
+        2_758_483_344, "profiles/prefill_kernel_global16_prefill_L5_Hkv8_D128_ctx131072.md"),
 }
 
 

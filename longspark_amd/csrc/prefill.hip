@@ -413,18 +413,44 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(const ls_prefill_a
   const int len = clamp_len(a, b);
   const int ns = (len + g.chunk - 1) / g.chunk;
 
+  // split maxima and sums across the lanes (lane s holds split s), then the
+  // output with the lanes owning 4 consecutive values of the row and four
+  // splits' partial rows in flight at a time
+  const float2* mz = reinterpret_cast<const float2*>(part_mz) + (ub * g.nsplit) * nrows + r;
   float mx = -__builtin_inff();
-  for (int s = 0; s < ns; ++s) mx = fmaxf(mx, part_mz[((ub * g.nsplit + s) * nrows + r) * 2]);
-  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int s = lane; s < ns; s += kWave) mx = fmaxf(mx, mz[static_cast<int64_t>(s) * nrows].x);
+  mx = wave_max(mx);
   float zs = 0.f;
+  for (int s = lane; s < ns; s += kWave) {
+    const float2 v = mz[static_cast<int64_t>(s) * nrows];
+    zs += v.y * __builtin_amdgcn_exp2f(v.x - mx);
+  }
+  zs = wave_sum(zs);
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
   const bool mine = lane * 4 < D;
-  for (int s = 0; s < ns; ++s) {
-    const int64_t prow = (ub * g.nsplit + s) * nrows + r;
-    const float2 mz = *reinterpret_cast<const float2*>(part_mz + prow * 2);
-    const float f = __builtin_amdgcn_exp2f(mz.x - mx);
-    zs += mz.y * f;
-    if (mine) {
-      const float4 v = *reinterpret_cast<const float4*>(part_o + prow * D + lane * 4);
+  if (mine) {
+    const float* po = part_o + ((ub * g.nsplit) * nrows + r) * D + lane * 4;
+    const int64_t sstride = static_cast<int64_t>(nrows) * D;
+    int s = 0;
+    for (; s + 4 <= ns; s += 4) {
+      float4 v[4];
+      float f[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        v[k] = *reinterpret_cast<const float4*>(po + (s + k) * sstride);
+        f[k] = __builtin_amdgcn_exp2f(mz[static_cast<int64_t>(s + k) * nrows].x - mx);
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        acc.x += v[k].x * f[k];
+        acc.y += v[k].y * f[k];
+        acc.z += v[k].z * f[k];
+        acc.w += v[k].w * f[k];
+      }
+    }
+    for (; s < ns; ++s) {
+      const float4 v = *reinterpret_cast<const float4*>(po + s * sstride);
+      const float f = __builtin_amdgcn_exp2f(mz[static_cast<int64_t>(s) * nrows].x - mx);
       acc.x += v.x * f;
       acc.y += v.y * f;
       acc.z += v.z * f;

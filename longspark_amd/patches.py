@@ -72,6 +72,10 @@ def replacements() -> Dict[str, Dict[str, object]]:
         "sglang.srt.speculative.global16_raw256_incremental": {
             "cache_position_scores": summary.cache_position_scores,
             "merge_accepted_positions_": summary.merge_accepted_positions_},
+        # prefill summary initialisation (SPEC/global16_raw256.py:668-784), a method of the
+        # verify context class: dotted names replace a class attribute
+        "sglang.srt.speculative.global16_raw256": {
+            "Global16Raw256VerifyContext.run_prefill_global_attention": summary.run_prefill_global_attention},
         # recent window (SPEC/global16_raw256_draft_fused.py:372-413, engine/draft.py:14-21)
         "sglang.srt.speculative.global16_raw256_draft_fused": {
             "build_raw256_page_table": kvwindow.build_raw256_page_table},
@@ -109,6 +113,9 @@ def install(modules: Optional[Iterable[str]] = None) -> Tuple[List[str], List[st
             skipped.append(name)
             continue
         for attr, fn in table[name].items():
-            setattr(mod, attr, fn)
+            owner, *path = [mod, *attr.split(".")]
+            for part in path[:-1]:
+                owner = getattr(owner, part)
+            setattr(owner, path[-1], fn)
         patched.append(name)
     return patched, skipped

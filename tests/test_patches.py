@@ -34,3 +34,22 @@ def test_every_replacement_target_is_listed_once():
     assert len(table) >= 8
     for mod, attrs in table.items():
         assert attrs and all(callable(f) for f in attrs.values()), mod
+
+
+def test_install_replaces_a_class_method(monkeypatch):
+    name = "sglang.srt.speculative.global16_raw256"
+    parts = name.split(".")
+    for i in range(1, len(parts) + 1):
+        mod = ".".join(parts[:i])
+        if mod not in sys.modules:
+            monkeypatch.setitem(sys.modules, mod, types.ModuleType(mod))
+
+    class Global16Raw256VerifyContext:
+        def run_prefill_global_attention(self, **kw):
+            raise AssertionError("reference body still installed")
+
+    monkeypatch.setattr(sys.modules[name], "Global16Raw256VerifyContext", Global16Raw256VerifyContext,
+                        raising=False)
+    patched, _ = patches.install([name])
+    assert patched == [name]
+    assert Global16Raw256VerifyContext.run_prefill_global_attention is summary.run_prefill_global_attention
