@@ -629,6 +629,51 @@ typedef struct ls_prefill_args {
 LS_API int ls_global16_prefill_workspace(const ls_prefill_args* args, int64_t* scratch_bytes);
 LS_API int ls_global16_prefill(const ls_prefill_args* args, void* scratch, int64_t scratch_bytes, void* stream);
 
+/* ---- Drafter attention over the refreshed views ----------------------------
+ * Replaces fused_global_local_raw_attention
+ * (SRT/speculative/global16_raw256_draft_all_attention.py:52-281,348-416):
+ * for each request and query head, 7 query rows attend over
+ *   Raw256  rows page_table[b, t] (t < raw_lengths[b]) of the page-size-1
+ *           key/value cache, scores (q.k) * scale;
+ *   Global16 16 rows per query head: keys global_keys[b][h], values the fp32
+ *           summary state global_values[state_slots[b]][h] rounded to bf16,
+ *           scores bf16(q.k) * scale;
+ *   Local7  7 rows per KV head with visibility local_mask[b][row][src],
+ *           scores bf16(q.k) * scale;
+ * folded as online-softmax steps in that order (raw in blocks of 64 rows),
+ * each step's weights entering the weighted sum of values as bf16.  Output
+ * bf16.  head_dim 128, bf16 tensors with a contiguous head dimension; every
+ * stride in elements.  At most 16 query heads per KV head. */
+typedef struct ls_draft_attention_args {
+  int64_t batch;
+  int32_t q_heads, kv_heads;
+  float softmax_scale;
+  const void* query;                   /* [B][Hq][7][128] bf16 */
+  int64_t q_stride_b, q_stride_h, q_stride_r;
+  const void* global_keys;             /* [B][Hq][16][128] bf16 */
+  int64_t gk_stride_b, gk_stride_h, gk_stride_g;
+  const float* global_values;          /* [C][Hq][16][128] fp32 (state pool) */
+  int64_t gv_stride_b, gv_stride_h, gv_stride_g;
+  const int32_t* state_slots;          /* [B] */
+  const void* local_keys;              /* [B][Hkv][7][128] bf16 */
+  int64_t lk_stride_b, lk_stride_h, lk_stride_l;
+  const void* local_values;            /* [B][Hkv][7][128] bf16 */
+  int64_t lv_stride_b, lv_stride_h, lv_stride_l;
+  const uint8_t* local_mask;           /* [B][7][7] bool */
+  int64_t lm_stride_b, lm_stride_r, lm_stride_l;
+  const void* key_cache;               /* [S][1][Hkv][128] bf16 */
+  int64_t kc_stride_s, kc_stride_h;
+  const void* value_cache;
+  int64_t vc_stride_s, vc_stride_h;
+  const int32_t* page_table;           /* [B][256] */
+  int64_t pt_stride_b;
+  const int32_t* raw_lengths;          /* [B], clamped to [0, 256] */
+  void* output;                        /* [B][Hq][7][128] bf16 */
+  int64_t o_stride_b, o_stride_h, o_stride_r;
+} ls_draft_attention_args;
+
+LS_API int ls_draft_attention(const ls_draft_attention_args* args, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

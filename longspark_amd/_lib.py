@@ -121,6 +121,24 @@ class PrefillArgs(ctypes.Structure):
     ]
 
 
+class DraftAttentionArgs(ctypes.Structure):
+    """Mirror of ``ls_draft_attention_args``."""
+    _fields_ = [
+        ("batch", I64), ("q_heads", I32), ("kv_heads", I32), ("softmax_scale", F32),
+        ("query", P), ("q_stride_b", I64), ("q_stride_h", I64), ("q_stride_r", I64),
+        ("global_keys", P), ("gk_stride_b", I64), ("gk_stride_h", I64), ("gk_stride_g", I64),
+        ("global_values", P), ("gv_stride_b", I64), ("gv_stride_h", I64), ("gv_stride_g", I64),
+        ("state_slots", P),
+        ("local_keys", P), ("lk_stride_b", I64), ("lk_stride_h", I64), ("lk_stride_l", I64),
+        ("local_values", P), ("lv_stride_b", I64), ("lv_stride_h", I64), ("lv_stride_l", I64),
+        ("local_mask", P), ("lm_stride_b", I64), ("lm_stride_r", I64), ("lm_stride_l", I64),
+        ("key_cache", P), ("kc_stride_s", I64), ("kc_stride_h", I64),
+        ("value_cache", P), ("vc_stride_s", I64), ("vc_stride_h", I64),
+        ("page_table", P), ("pt_stride_b", I64), ("raw_lengths", P),
+        ("output", P), ("o_stride_b", I64), ("o_stride_h", I64), ("o_stride_r", I64),
+    ]
+
+
 # name -> (restype, argtypes).  Kept in the order of include/longspark_amd.h.
 _SIGNATURES = {
     "ls_last_error": (c_char_p, []),
@@ -155,6 +173,7 @@ _SIGNATURES = {
     "ls_summary_update": (I32, [ctypes.POINTER(SummaryArgs), P]),
     "ls_global16_prefill_workspace": (I32, [ctypes.POINTER(PrefillArgs), P]),
     "ls_global16_prefill": (I32, [ctypes.POINTER(PrefillArgs), P, I64, P]),
+    "ls_draft_attention": (I32, [ctypes.POINTER(DraftAttentionArgs), P]),
 }
 
 for _name, (_res, _args) in _SIGNATURES.items():

@@ -1,0 +1,310 @@
+// Drafter attention over the three refreshed views in one kernel:
+// Raw256 (the recent window, read through the request's page-table row),
+// Global16 (the summary state) and Local7 (the in-block rows).
+//
+// Reference: SRT/speculative/global16_raw256_draft_all_attention.py:52-281
+// (one Triton program per (request, query head)); SRT =
+// vendor/sglang/python/sglang/srt.  For every query row (7 per head) the
+// sources are folded in the reference's order, each as one online-softmax step
+// (running maximum m, sum z, unnormalised output o):
+//   raw     blocks of 64 window rows, scores = (q . k) * scale (fp32),
+//           rows at or past raw_lengths[b] invisible;
+//   global  16 rows per query head, scores = bf16(q . k) * scale;
+//           values = the fp32 summary state rounded to bf16;
+//   local   7 rows per KV head, scores = bf16(q . k) * scale, visibility
+//           from the request's 7 x 7 mask.
+// In every step the weights exp(s - m) enter the weighted sum of values as
+// bf16 and the sum z as fp32, as the reference does; out = o / z in bf16.
+//
+// Here one workgroup serves (request, KV head): one wave per query head of
+// the group, so each raw key/value row is read from HBM once for all of
+// them (the reference reads it once per query head).  Raw rows are staged in
+// LDS (keys as they are, values transposed to [d][row]); the products run on
+// v_mfma_f32_16x16x32_bf16 with the 7 query rows padded to 16:
+//   S^T[16 src x 16 rows] = K[16 x 128] . Q^T,   O^T += V^T[16 x 32] . P^T[32 x 16]
+// (the lane holding row c16 gets sources 4*g16 + i of each 16-source tile).
+#include "mfma_tile.h"
+
+namespace ls {
+namespace {
+
+constexpr int kD = 128;          // head_dim
+constexpr int kRows = 7;         // query rows per head
+constexpr int kGlobal = 16;      // summary rows per query head
+constexpr int kLocal = 7;        // in-block rows per KV head
+constexpr int kRaw = 256;        // window rows
+constexpr int kBlk = 64;         // window rows per step (the reference's block)
+constexpr int kChunks = kD / 8;  // 16-byte vectors per row
+constexpr int kKP = kD + 8;      // 16-bit elements per LDS key row
+constexpr int kVP = kBlk + 4;    // 16-bit elements per LDS transposed value row
+constexpr int kMinThreads = 256;
+constexpr int kKR = kBlk * kChunks / kMinThreads;         // key vectors per thread per step (4)
+constexpr int kVR = (kBlk / 2) * kChunks / kMinThreads;   // value pairs per thread per step (2)
+constexpr int kKB = kD / 32;
+constexpr int kDB = kD / 16;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr size_t kLds = static_cast<size_t>(kBlk) * kKP * 2 + static_cast<size_t>(kD) * kVP * 2;
+
+__device__ __forceinline__ float round_bf16(float x) { return to_f32<uint16_t>(from_f32<uint16_t>(x)); }
+
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+  typedef __attribute__((ext_vector_type(2))) float f32x2;
+  typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
+  const f32x2 v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+}
+
+__device__ __forceinline__ uint32_t half16(const uint4& v, int e) {
+  const uint32_t w = e < 2 ? v.x : (e < 4 ? v.y : (e < 6 ? v.z : v.w));
+  return (e & 1) ? (w >> 16) : (w & 0xffffu);
+}
+
+// Online-softmax state of the lane's query row (the 4 lanes of a row hold
+// the same m; z is a per-lane partial sum).
+struct RowState {
+  f32x4_t o[kDB];
+  float m, z;
+};
+
+// Fold one 16-or-32-source tile of base-2 scores into the row state.
+// sc[t][i]: score of source t*16 + 4*g16 + i (-inf when invisible);
+// vt(db, t) returns the A operand half (4 bf16 values of sources
+// t*16 + 4*g16 .. +3 at column db*16 + c16) for tile t.
+template <int kTiles, typename VT>
+__device__ __forceinline__ void fold(RowState& st, f32x4_t (&sc)[kTiles], VT vt) {
+  float bm = -__builtin_inff();
+#pragma unroll
+  for (int t = 0; t < kTiles; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) bm = fmaxf(bm, sc[t][i]);
+  bm = fmaxf(bm, __shfl_xor(bm, 16, kWave));
+  bm = fmaxf(bm, __shfl_xor(bm, 32, kWave));
+  const float mn = fmaxf(st.m, bm);
+  // a row with nothing visible yet keeps m = -inf: subtract 0 instead
+  const float base = mn == -__builtin_inff() ? 0.f : mn;
+  const float alpha = __builtin_amdgcn_exp2f(st.m - base);
+  st.m = mn;
+  st.z *= alpha;
+#pragma unroll
+  for (int db = 0; db < kDB; ++db) st.o[db] *= alpha;
+  float p[kTiles][4];
+#pragma unroll
+  for (int t = 0; t < kTiles; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      p[t][i] = __builtin_amdgcn_exp2f(sc[t][i] - base);
+      st.z += p[t][i];
+    }
+#pragma unroll
+  for (int kb = 0; kb < (kTiles + 1) / 2; ++kb) {
+    uint4 pb;
+    pb.x = pack_bf16(p[2 * kb][0], p[2 * kb][1]);
+    pb.y = pack_bf16(p[2 * kb][2], p[2 * kb][3]);
+    if (2 * kb + 1 < kTiles) {
+      pb.z = pack_bf16(p[(2 * kb + 1) % kTiles][0], p[(2 * kb + 1) % kTiles][1]);
+      pb.w = pack_bf16(p[(2 * kb + 1) % kTiles][2], p[(2 * kb + 1) % kTiles][3]);
+    } else {
+      pb.z = 0u;
+      pb.w = 0u;
+    }
+#pragma unroll
+    for (int db = 0; db < kDB; ++db) {
+      const uint2 lo = vt(db, 2 * kb);
+      const uint2 hi = 2 * kb + 1 < kTiles ? vt(db, 2 * kb + 1) : make_uint2(0u, 0u);
+      st.o[db] = Mma<BF16>::run(make_uint4(lo.x, lo.y, hi.x, hi.y), pb, st.o[db]);
+    }
+  }
+}
+
+__global__ __launch_bounds__(1024) void draft_attention_kernel(const ls_draft_attention_args a, int threads) {
+  extern __shared__ __align__(16) char smem[];
+  uint16_t* kls = reinterpret_cast<uint16_t*>(smem);
+  uint16_t* vls = kls + kBlk * kKP;
+
+  const int64_t b = blockIdx.x / a.kv_heads;
+  const int kvh = static_cast<int>(blockIdx.x % a.kv_heads);
+  const int groups = a.q_heads / a.kv_heads;
+  const int tid = threadIdx.x, nthr = threads;
+  const int lane = tid % kWave, wave = tid / kWave;
+  const int g16 = lane >> 4, c16 = lane & 15;
+  const bool head_wave = wave < groups;
+  const int head = kvh * groups + (head_wave ? wave : 0);
+  const bool row_ok = c16 < kRows;
+  const float scale2 = a.softmax_scale * kLog2e;
+
+  // Query row c16 of this wave's head as the B operand (rows 7..15 zero).
+  uint4 qb[kKB];
+  {
+    const uint16_t* q = static_cast<const uint16_t*>(a.query) + b * a.q_stride_b + head * a.q_stride_h +
+                        (row_ok ? c16 : 0) * a.q_stride_r;
+#pragma unroll
+    for (int kb = 0; kb < kKB; ++kb) {
+      const uint4 v = load16(q + kb * 32 + g16 * 8);
+      qb[kb] = row_ok ? v : make_uint4(0u, 0u, 0u, 0u);
+    }
+  }
+  RowState st;
+#pragma unroll
+  for (int db = 0; db < kDB; ++db) st.o[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  st.m = -__builtin_inff();
+  st.z = 0.f;
+
+  // ---- raw window: ceil(len / 64) steps through the page-table row ----
+  int raw_len = a.raw_lengths[b];
+  raw_len = raw_len < 0 ? 0 : (raw_len > kRaw ? kRaw : raw_len);
+  const char* kbase = static_cast<const char*>(a.key_cache) + kvh * a.kc_stride_h * 2;
+  const char* vbase = static_cast<const char*>(a.value_cache) + kvh * a.vc_stride_h * 2;
+  const int32_t* pt = a.page_table + b * a.pt_stride_b;
+  for (int tb = 0; tb < raw_len; tb += kBlk) {
+    // loads first (no branch around them; rows past the window read row
+    // raw_len - 1 and get weight 0), then the LDS stores
+    uint4 kr[kKR], vr[kVR][2];
+#pragma unroll
+    for (int i = 0; i < kKR; ++i) {
+      const int j = min(i * nthr + tid, kBlk * kChunks - 1);
+      const int64_t loc = pt[min(tb + j / kChunks, raw_len - 1)];
+      kr[i] = load16_global(kbase + (loc * a.kc_stride_s + (j % kChunks) * 8) * 2);
+    }
+#pragma unroll
+    for (int i = 0; i < kVR; ++i) {
+      const int v = min(i * nthr + tid, (kBlk / 2) * kChunks - 1);
+      const int p2 = v % (kBlk / 2), c = v / (kBlk / 2);
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int64_t loc = pt[min(tb + 2 * p2 + e, raw_len - 1)];
+        vr[i][e] = load16_global(vbase + (loc * a.vc_stride_s + c * 8) * 2);
+      }
+    }
+    lds_barrier();  // previous step's reads done
+#pragma unroll
+    for (int i = 0; i < kKR; ++i) {
+      const int j = i * nthr + tid;
+      if (j < kBlk * kChunks) *reinterpret_cast<uint4*>(kls + (j / kChunks) * kKP + (j % kChunks) * 8) = kr[i];
+    }
+#pragma unroll
+    for (int i = 0; i < kVR; ++i) {
+      const int v = i * nthr + tid;
+      if (v < (kBlk / 2) * kChunks) {
+        const int p2 = v % (kBlk / 2), c = v / (kBlk / 2);
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          *reinterpret_cast<uint32_t*>(vls + (c * 8 + e) * kVP + 2 * p2) =
+              half16(vr[i][0], e) | (half16(vr[i][1], e) << 16);
+      }
+    }
+    lds_barrier();
+    if (!head_wave) continue;
+    f32x4_t sc[kBlk / 16];
+#pragma unroll
+    for (int t = 0; t < kBlk / 16; ++t) {
+      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kb = 0; kb < kKB; ++kb)
+        acc = Mma<BF16>::run(*reinterpret_cast<const uint4*>(kls + (t * 16 + c16) * kKP + kb * 32 + g16 * 8),
+                             qb[kb], acc);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        sc[t][i] = tb + t * 16 + 4 * g16 + i < raw_len ? acc[i] * scale2 : -__builtin_inff();
+    }
+    fold<kBlk / 16>(st, sc, [&](int db, int t) __attribute__((always_inline)) {
+      return *reinterpret_cast<const uint2*>(vls + (db * 16 + c16) * kVP + t * 16 + 4 * g16);
+    });
+  }
+  if (!head_wave) return;
+
+  // ---- global: 16 summary rows of this query head ----
+  {
+    const uint16_t* gk = static_cast<const uint16_t*>(a.global_keys) + b * a.gk_stride_b + head * a.gk_stride_h +
+                         c16 * a.gk_stride_g;
+    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kb = 0; kb < kKB; ++kb) acc = Mma<BF16>::run(load16(gk + kb * 32 + g16 * 8), qb[kb], acc);
+    f32x4_t sc[1];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sc[0][i] = round_bf16(acc[i]) * a.softmax_scale * kLog2e;
+    const int64_t slot = a.state_slots[b];
+    const float* gv = a.global_values + slot * a.gv_stride_b + head * a.gv_stride_h;
+    fold<1>(st, sc, [&](int db, int) __attribute__((always_inline)) {
+      const float* col = gv + (4 * g16) * a.gv_stride_g + db * 16 + c16;
+      return make_uint2(pack_bf16(col[0], col[a.gv_stride_g]), pack_bf16(col[2 * a.gv_stride_g], col[3 * a.gv_stride_g]));
+    });
+  }
+
+  // ---- local: 7 in-block rows of this KV head, per-row visibility ----
+  {
+    const uint16_t* lk = static_cast<const uint16_t*>(a.local_keys) + b * a.lk_stride_b + kvh * a.lk_stride_h +
+                         (c16 < kLocal ? c16 : 0) * a.lk_stride_l;
+    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kb = 0; kb < kKB; ++kb) {
+      const uint4 v = load16(lk + kb * 32 + g16 * 8);
+      acc = Mma<BF16>::run(c16 < kLocal ? v : make_uint4(0u, 0u, 0u, 0u), qb[kb], acc);
+    }
+    f32x4_t sc[1];
+    const uint8_t* mrow = a.local_mask + b * a.lm_stride_b + (row_ok ? c16 : 0) * a.lm_stride_r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int src = 4 * g16 + i;
+      const bool vis = row_ok && src < kLocal && mrow[(src < kLocal ? src : 0) * a.lm_stride_l] != 0;
+      sc[0][i] = vis ? round_bf16(acc[i]) * a.softmax_scale * kLog2e : -__builtin_inff();
+    }
+    const uint16_t* lv = static_cast<const uint16_t*>(a.local_values) + b * a.lv_stride_b + kvh * a.lv_stride_h;
+    fold<1>(st, sc, [&](int db, int) __attribute__((always_inline)) {
+      uint32_t h[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int src = 4 * g16 + e;
+        h[e] = src < kLocal ? lv[src * a.lv_stride_l + db * 16 + c16] : 0u;
+      }
+      return make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+    });
+  }
+
+  float z = st.z;
+  z += __shfl_xor(z, 16, kWave);
+  z += __shfl_xor(z, 32, kWave);
+  if (!row_ok) return;
+  const float inv = 1.f / z;
+  uint16_t* out = static_cast<uint16_t*>(a.output) + b * a.o_stride_b + head * a.o_stride_h + c16 * a.o_stride_r;
+#pragma unroll
+  for (int db = 0; db < kDB; ++db) {
+    uint2 w;
+    w.x = pack_bf16(st.o[db][0] * inv, st.o[db][1] * inv);
+    w.y = pack_bf16(st.o[db][2] * inv, st.o[db][3] * inv);
+    *reinterpret_cast<uint2*>(out + db * 16 + 4 * g16) = w;
+  }
+}
+
+}  // namespace
+}  // namespace ls
+
+extern "C" int ls_draft_attention(const ls_draft_attention_args* args, void* stream) {
+  using namespace ls;
+  const char* what = "ls_draft_attention";
+  LS_CHECK(args != nullptr, LS_ERR_VALUE, "%s: null argument block", what);
+  const ls_draft_attention_args& a = *args;
+  LS_CHECK(a.batch >= 0 && a.q_heads >= 1 && a.kv_heads >= 1 && a.q_heads % a.kv_heads == 0, LS_ERR_SHAPE,
+           "%s: query heads must be a positive multiple of KV heads", what);
+  LS_CHECK(a.q_heads / a.kv_heads <= 16, LS_ERR_SHAPE, "%s: at most 16 query heads per KV head", what);
+  LS_CHECK(a.softmax_scale > 0.f, LS_ERR_VALUE, "%s: softmax_scale must be > 0", what);
+  if (a.batch == 0) return LS_OK;
+  LS_CHECK(a.query && a.global_keys && a.global_values && a.state_slots && a.local_keys && a.local_values &&
+               a.local_mask && a.key_cache && a.value_cache && a.page_table && a.raw_lengths && a.output,
+           LS_ERR_VALUE, "%s: every tensor is required", what);
+  LS_CHECK(aligned16(a.query) && aligned16(a.global_keys) && aligned16(a.local_keys) && aligned16(a.key_cache) &&
+               aligned16(a.value_cache) && aligned16(a.output) && a.q_stride_b % 8 == 0 && a.q_stride_h % 8 == 0 &&
+               a.q_stride_r % 8 == 0 && a.gk_stride_b % 8 == 0 && a.gk_stride_h % 8 == 0 &&
+               a.gk_stride_g % 8 == 0 && a.lk_stride_b % 8 == 0 && a.lk_stride_h % 8 == 0 &&
+               a.lk_stride_l % 8 == 0 && a.kc_stride_s % 8 == 0 && a.kc_stride_h % 8 == 0 &&
+               a.vc_stride_s % 8 == 0 && a.vc_stride_h % 8 == 0 && a.o_stride_b % 4 == 0 &&
+               a.o_stride_h % 4 == 0 && a.o_stride_r % 4 == 0,
+           LS_ERR_ALIGN, "%s: 16-bit rows must be 16-byte aligned (output rows 8-byte aligned)", what);
+  const int64_t grid = a.batch * a.kv_heads;
+  LS_CHECK(grid < (int64_t(1) << 31), LS_ERR_SHAPE, "%s: grid too large", what);
+  const int groups = a.q_heads / a.kv_heads;
+  const int threads = (groups < 4 ? 4 : groups) * kWave;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  draft_attention_kernel<<<dim3(static_cast<unsigned>(grid)), threads, kLds, st>>>(a, threads);
+  LS_LAUNCH_CHECK();
+  return LS_OK;
+}
