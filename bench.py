@@ -45,6 +45,7 @@ TRAFFIC = {
     "chain_kernel": (158_497_097, "profiles/chain_kernel_chain_sampling_B128_K16_V151936.md"),
     "request_bias_kernel": (1_403_662_037, "profiles/request_bias_kernel_adjust_logits_B128_K16_V151936.md"),
     "sample_step_kernel": (156_653_721, "profiles/sample_step_kernel_B128_V151936.md"),
+    "draft_attention_kernel": (204_226_688, "profiles/draft_attention_kernel_B128_Hq32_Hkv8_raw256.md"),
     "prefill_kernel + prefill_combine_kernel": (
         2_758_483_344, "profiles/prefill_kernel_global16_prefill_L5_Hkv8_D128_ctx131072.md"),
 }
@@ -648,6 +649,66 @@ class Global16Prefill:
                 "sample": f"one layer, prefix {n}, oracle torch-CPU fp32 attention, median of {reps} runs"}
 
 
+class DraftAttention:
+    """fused_global_local_raw_attention: one drafter attention step over the
+    three views for a batch of 128 requests, 32 query and 8 KV heads,
+    head_dim 128, 7 query rows; every request's Raw256 window full (256 rows,
+    page size 1, rows scattered over a pool of 128 x 256 slots), 16 summary
+    rows per query head from the fp32 state, 7 local rows under a causal
+    in-block mask."""
+
+    name = "draft_attention"
+    metric = "drafter attention GB/s (algorithmic bytes) at B=128, 32 Hq / 8 Hkv, D 128, Raw256 + Global16 + Local7"
+    unit = "GB/s"
+    dtype = "bf16"
+
+    def __init__(self, dev, batch=128, q_heads=32, kv_heads=8):
+        g = torch.Generator(device=dev).manual_seed(63)
+        self.batch, self.q_heads, self.kv_heads = batch, q_heads, kv_heads
+        bf = torch.bfloat16
+        self.q = (0.3 * torch.randn(batch, q_heads, 7, 128, generator=g, device=dev)).to(bf)
+        self.gk = (0.3 * torch.randn(batch, q_heads, 16, 128, generator=g, device=dev)).to(bf)
+        self.gv = torch.randn(batch, q_heads, 16, 128, generator=g, device=dev)
+        self.slots = torch.arange(batch, dtype=torch.int32, device=dev)
+        self.lk = (0.3 * torch.randn(batch, kv_heads, 7, 128, generator=g, device=dev)).to(bf)
+        self.lv = torch.randn(batch, kv_heads, 7, 128, generator=g, device=dev).to(bf)
+        self.mask = torch.ones(7, 7, dtype=torch.bool, device=dev).tril().expand(batch, 7, 7).contiguous()
+        pool = batch * 256
+        self.kc = (0.3 * torch.randn(pool, 1, kv_heads, 128, generator=g, device=dev)).to(bf)
+        self.vc = torch.randn(pool, 1, kv_heads, 128, generator=g, device=dev).to(bf)
+        self.pt = torch.randperm(pool, generator=g, device=dev).to(torch.int32).view(batch, 256)
+        self.rl = torch.full((batch,), 256, dtype=torch.int32, device=dev)
+        self.out = torch.empty_like(self.q)
+        raw = 2 * batch * kv_heads * 256 * 128 * 2
+        per_head = 16 * 128 * 2 + 16 * 128 * 4 + 2 * 7 * 128 * 2      # summary keys, fp32 state, query + output
+        self.bytes = raw + batch * q_heads * per_head + 2 * self.lk.numel() * 2 + self.pt.numel() * 4 \
+            + self.mask.numel()
+        self.units = self.bytes / 1e9
+        self.kernel = "draft_attention_kernel"
+
+    def step(self):
+        from longspark_amd import draft_attention
+        return draft_attention.fused_global_local_raw_attention(
+            query=self.q, global_keys=self.gk, global_values=self.gv, state_slots=self.slots, local_keys=self.lk,
+            local_values=self.lv, local_attention_mask=self.mask, key_cache=self.kc, value_cache=self.vc,
+            page_table=self.pt, raw_lengths=self.rl, output=self.out, softmax_scale=128 ** -0.5)
+
+    def config(self):
+        return {"workload": f"drafter attention B={self.batch} Hq={self.q_heads} Hkv={self.kv_heads} D=128, "
+                            "7 rows over Raw256 (full) + Global16 + Local7", "batch": self.batch}
+
+    def cpu_baseline(self, threads):
+        from oracle import draft_attention as oda
+        torch.set_num_threads(threads)
+        b = 2
+        args = [t[:b].cpu() for t in (self.q, self.gk, self.gv)] + [torch.arange(b, dtype=torch.int32)] + \
+               [t[:b].cpu() for t in (self.lk, self.lv, self.mask)] + [self.kc.cpu(), self.vc.cpu()] + \
+               [t[:b].cpu() for t in (self.pt, self.rl)]
+        med, n = time_cpu(lambda: oda.fused_global_local_raw_attention(*args, 128 ** -0.5))
+        return {"value": self.bytes * b / self.batch / med / 1e9, "threads": threads,
+                "sample": f"{b} requests, oracle torch-CPU per (request, query head), median of {n} runs"}
+
+
 class FullRound:
     """One verify-and-refresh round at Qwen3-14B geometry: 40 layers, 40 query
     and 8 KV heads, head_dim 128, vocab 151,936, batch 128, block 16, contexts
@@ -817,8 +878,8 @@ class AdjustLogits:
 
 
 WORKLOADS = {w.name: w for w in (GreedyVerify, StochasticVerify, WindowGather, SummaryUpdate, SoftmaxTempWorkload,
-                                  TargetProbsWorkload, ChainSampling, AdjustLogits, SampleStep, Global16Prefill, FullRound,
-                                  HbmCopy)}
+                                  TargetProbsWorkload, ChainSampling, AdjustLogits, SampleStep, Global16Prefill, DraftAttention,
+                                  FullRound, HbmCopy)}
 DEFAULT_WORKLOAD = "verify_sample"
 
 

@@ -19,7 +19,7 @@ from typing import Dict, Iterable, List, Optional, Tuple
 
 def replacements() -> Dict[str, Dict[str, object]]:
     """module name -> {attribute: replacement}, for every hot-path call site."""
-    from . import accept, dense, kvwindow, penalties, sample, summary, verify
+    from . import accept, dense, draft_attention, kvwindow, penalties, sample, summary, verify
 
     return {
         # greedy verify (SPEC/dspark_components/kernels/accept_greedy.py:22-60)
@@ -76,6 +76,11 @@ def replacements() -> Dict[str, Dict[str, object]]:
         # verify context class: dotted names replace a class attribute
         "sglang.srt.speculative.global16_raw256": {
             "Global16Raw256VerifyContext.run_prefill_global_attention": summary.run_prefill_global_attention},
+        # drafter attention over the three views (SPEC/global16_raw256_draft_all_attention.py:283-416;
+        # SPEC/global16_raw256.py:119-128 imports it at call time)
+        "sglang.srt.speculative.global16_raw256_draft_all_attention": {
+            "fused_global_local_raw_attention": draft_attention.fused_global_local_raw_attention,
+            "can_use_fused_global_local_raw_attention": draft_attention.can_use_fused_global_local_raw_attention},
         # recent window (SPEC/global16_raw256_draft_fused.py:372-413, engine/draft.py:14-21)
         "sglang.srt.speculative.global16_raw256_draft_fused": {
             "build_raw256_page_table": kvwindow.build_raw256_page_table},
