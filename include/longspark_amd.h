@@ -670,9 +670,30 @@ typedef struct ls_draft_attention_args {
   const int32_t* raw_lengths;          /* [B], clamped to [0, 256] */
   void* output;                        /* [B][Hq][7][128] bf16 */
   int64_t o_stride_b, o_stride_h, o_stride_r;
+  /* ls_draft_merge only: the window attention computed elsewhere (FA3 in the
+   * reference) as output [B*7][Hq][128] bf16 and natural-log LSE [B*7][Hq]
+   * fp32 (token row b*7 + r), and the softcap of the summary/local scores */
+  const void* raw_output;
+  int64_t ro_stride_t, ro_stride_h;
+  const float* raw_lse;
+  int64_t rl_stride_t, rl_stride_h;
+  float softcap;
 } ls_draft_attention_args;
 
 LS_API int ls_draft_attention(const ls_draft_attention_args* args, void* stream);
+
+/* Replaces fused_global_local_raw_merge
+ * (SRT/speculative/global16_raw256_draft_fused.py:72-312,417-479), the
+ * reference's default drafter path after its FA3 window attention: the
+ * Global16 and Local7 sources are each normalised on their own (weighted sum
+ * of bf16 weights and values rounded to bf16, divided by the fp32 sum; scores
+ * bf16(q.k) * scale, then softcap * tanh(s / softcap) when softcap > 0), and
+ * the three outputs are merged by their LSEs:
+ *   out = (raw * e^(lse_r - M) + global * e^(lse_g - M) + local * e^(lse_l - M)) / sum,
+ * M the largest LSE, a row with no visible local row leaving that term out.
+ * Uses every field of ls_draft_attention_args except key_cache, value_cache,
+ * page_table and raw_lengths. */
+LS_API int ls_draft_merge(const ls_draft_attention_args* args, void* stream);
 
 #ifdef __cplusplus
 }

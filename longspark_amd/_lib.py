@@ -136,6 +136,8 @@ class DraftAttentionArgs(ctypes.Structure):
         ("value_cache", P), ("vc_stride_s", I64), ("vc_stride_h", I64),
         ("page_table", P), ("pt_stride_b", I64), ("raw_lengths", P),
         ("output", P), ("o_stride_b", I64), ("o_stride_h", I64), ("o_stride_r", I64),
+        ("raw_output", P), ("ro_stride_t", I64), ("ro_stride_h", I64),
+        ("raw_lse", P), ("rl_stride_t", I64), ("rl_stride_h", I64), ("softcap", F32),
     ]
 
 
@@ -174,6 +176,7 @@ _SIGNATURES = {
     "ls_global16_prefill_workspace": (I32, [ctypes.POINTER(PrefillArgs), P]),
     "ls_global16_prefill": (I32, [ctypes.POINTER(PrefillArgs), P, I64, P]),
     "ls_draft_attention": (I32, [ctypes.POINTER(DraftAttentionArgs), P]),
+    "ls_draft_merge": (I32, [ctypes.POINTER(DraftAttentionArgs), P]),
 }
 
 for _name, (_res, _args) in _SIGNATURES.items():

@@ -275,6 +275,178 @@ __global__ __launch_bounds__(1024) void draft_attention_kernel(const ls_draft_at
   }
 }
 
+// ---------------------------------------------------------------------------
+// Merge form (SRT/speculative/global16_raw256_draft_fused.py:72-312): the
+// window attention arrives as (raw_output, raw_lse); the summary and local
+// sources are normalised on their own and the three merged by their LSEs.
+// One wave per query head; no LDS.
+
+// Weighted sum of one 16-source tile: O^T[16 d x 16 rows] = V^T . P^T with
+// the bf16 weights w[i] of sources 4*g16 + i (the second 16-source half of
+// the 32-deep product is zero).
+template <typename VT>
+__device__ __forceinline__ void tile_output(f32x4_t (&o)[kDB], const float (&w)[4], VT vt) {
+  uint4 pb;
+  pb.x = pack_bf16(w[0], w[1]);
+  pb.y = pack_bf16(w[2], w[3]);
+  pb.z = 0u;
+  pb.w = 0u;
+#pragma unroll
+  for (int db = 0; db < kDB; ++db) {
+    const uint2 lo = vt(db);
+    o[db] = Mma<BF16>::run(make_uint4(lo.x, lo.y, 0u, 0u), pb, f32x4_t{0.f, 0.f, 0.f, 0.f});
+  }
+}
+
+__device__ __forceinline__ float row_max4(float v) {
+  v = fmaxf(v, __shfl_xor(v, 16, kWave));
+  return fmaxf(v, __shfl_xor(v, 32, kWave));
+}
+__device__ __forceinline__ float row_sum4(float v) {
+  v += __shfl_xor(v, 16, kWave);
+  return v + __shfl_xor(v, 32, kWave);
+}
+
+__global__ __launch_bounds__(1024) void draft_merge_kernel(const ls_draft_attention_args a) {
+  const int64_t b = blockIdx.x / a.kv_heads;
+  const int kvh = static_cast<int>(blockIdx.x % a.kv_heads);
+  const int groups = a.q_heads / a.kv_heads;
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int g16 = lane >> 4, c16 = lane & 15;
+  const int head = kvh * groups + wave;
+  const bool row_ok = c16 < kRows;
+  const float cap = a.softcap;
+  auto finish = [&](float t) __attribute__((always_inline)) {
+    float s = round_bf16(t) * a.softmax_scale;
+    if (cap > 0.f) s = tanhf(s / cap) * cap;
+    return s;
+  };
+
+  uint4 qb[kKB];
+  {
+    const uint16_t* q = static_cast<const uint16_t*>(a.query) + b * a.q_stride_b + head * a.q_stride_h +
+                        (row_ok ? c16 : 0) * a.q_stride_r;
+#pragma unroll
+    for (int kb = 0; kb < kKB; ++kb) {
+      const uint4 v = load16(q + kb * 32 + g16 * 8);
+      qb[kb] = row_ok ? v : make_uint4(0u, 0u, 0u, 0u);
+    }
+  }
+
+  // ---- global: normalised over its 16 rows ----
+  f32x4_t go[kDB];
+  float glse;
+  {
+    const uint16_t* gk = static_cast<const uint16_t*>(a.global_keys) + b * a.gk_stride_b + head * a.gk_stride_h +
+                         c16 * a.gk_stride_g;
+    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kb = 0; kb < kKB; ++kb) acc = Mma<BF16>::run(load16(gk + kb * 32 + g16 * 8), qb[kb], acc);
+    float sc[4], w[4];
+    float mx = -__builtin_inff();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      sc[i] = finish(acc[i]);
+      mx = fmaxf(mx, sc[i]);
+    }
+    mx = row_max4(mx);
+    float z = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      w[i] = expf(sc[i] - mx);
+      z += w[i];
+    }
+    z = row_sum4(z);
+    const int64_t slot = a.state_slots[b];
+    const float* gv = a.global_values + slot * a.gv_stride_b + head * a.gv_stride_h;
+    tile_output(go, w, [&](int db) __attribute__((always_inline)) {
+      const float* col = gv + (4 * g16) * a.gv_stride_g + db * 16 + c16;
+      return make_uint2(pack_bf16(col[0], col[a.gv_stride_g]),
+                        pack_bf16(col[2 * a.gv_stride_g], col[3 * a.gv_stride_g]));
+    });
+#pragma unroll
+    for (int db = 0; db < kDB; ++db)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) go[db][i] = round_bf16(go[db][i]) / z;
+    glse = mx + logf(z);
+  }
+
+  // ---- local: normalised over its visible rows (none: left out) ----
+  f32x4_t lo[kDB];
+  float llse;
+  bool has;
+  {
+    const uint16_t* lk = static_cast<const uint16_t*>(a.local_keys) + b * a.lk_stride_b + kvh * a.lk_stride_h +
+                         (c16 < kLocal ? c16 : 0) * a.lk_stride_l;
+    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kb = 0; kb < kKB; ++kb) {
+      const uint4 v = load16(lk + kb * 32 + g16 * 8);
+      acc = Mma<BF16>::run(c16 < kLocal ? v : make_uint4(0u, 0u, 0u, 0u), qb[kb], acc);
+    }
+    const uint8_t* mrow = a.local_mask + b * a.lm_stride_b + (row_ok ? c16 : 0) * a.lm_stride_r;
+    bool vis[4];
+    float sc[4], w[4];
+    float mx = -__builtin_inff(), nvis = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int src = 4 * g16 + i;
+      vis[i] = row_ok && src < kLocal && mrow[(src < kLocal ? src : 0) * a.lm_stride_l] != 0;
+      sc[i] = vis[i] ? finish(acc[i]) : -__builtin_inff();
+      mx = fmaxf(mx, sc[i]);
+      nvis += vis[i] ? 1.f : 0.f;
+    }
+    mx = row_max4(mx);
+    has = row_sum4(nvis) > 0.f;
+    const float safe = has ? mx : 0.f;
+    float z = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      w[i] = vis[i] ? expf(sc[i] - safe) : 0.f;
+      z += w[i];
+    }
+    z = row_sum4(z);
+    const float safe_z = has ? z : 1.f;
+    const uint16_t* lv = static_cast<const uint16_t*>(a.local_values) + b * a.lv_stride_b + kvh * a.lv_stride_h;
+    tile_output(lo, w, [&](int db) __attribute__((always_inline)) {
+      uint32_t h[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int src = 4 * g16 + e;
+        h[e] = src < kLocal ? lv[src * a.lv_stride_l + db * 16 + c16] : 0u;
+      }
+      return make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+    });
+#pragma unroll
+    for (int db = 0; db < kDB; ++db)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) lo[db][i] = round_bf16(lo[db][i]) / safe_z;
+    llse = has ? safe + logf(safe_z) : -__builtin_inff();
+  }
+
+  // ---- merge with the window attention by LSE ----
+  if (!row_ok) return;
+  const int64_t tok = b * kRows + c16;
+  const float rlse = a.raw_lse[tok * a.rl_stride_t + head * a.rl_stride_h];
+  const float mm = fmaxf(rlse, fmaxf(glse, llse));
+  const float rw = expf(rlse - mm), gw = expf(glse - mm), lw = has ? expf(llse - mm) : 0.f;
+  const float norm = rw + gw + lw;
+  const uint16_t* ro = static_cast<const uint16_t*>(a.raw_output) + tok * a.ro_stride_t + head * a.ro_stride_h;
+  uint16_t* out = static_cast<uint16_t*>(a.output) + b * a.o_stride_b + head * a.o_stride_h + c16 * a.o_stride_r;
+#pragma unroll
+  for (int db = 0; db < kDB; ++db) {
+    const uint2 rv = *reinterpret_cast<const uint2*>(ro + db * 16 + 4 * g16);
+    float r4[4] = {bf16_lo(rv.x), bf16_hi(rv.x), bf16_lo(rv.y), bf16_hi(rv.y)};
+    float y[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) y[i] = (r4[i] * rw + go[db][i] * gw + lo[db][i] * lw) / norm;
+    uint2 w;
+    w.x = pack_bf16(y[0], y[1]);
+    w.y = pack_bf16(y[2], y[3]);
+    *reinterpret_cast<uint2*>(out + db * 16 + 4 * g16) = w;
+  }
+}
+
 }  // namespace
 }  // namespace ls
 
@@ -305,6 +477,35 @@ extern "C" int ls_draft_attention(const ls_draft_attention_args* args, void* str
   const int threads = (groups < 4 ? 4 : groups) * kWave;
   hipStream_t st = static_cast<hipStream_t>(stream);
   draft_attention_kernel<<<dim3(static_cast<unsigned>(grid)), threads, kLds, st>>>(a, threads);
+  LS_LAUNCH_CHECK();
+  return LS_OK;
+}
+
+extern "C" int ls_draft_merge(const ls_draft_attention_args* args, void* stream) {
+  using namespace ls;
+  const char* what = "ls_draft_merge";
+  LS_CHECK(args != nullptr, LS_ERR_VALUE, "%s: null argument block", what);
+  const ls_draft_attention_args& a = *args;
+  LS_CHECK(a.batch >= 0 && a.q_heads >= 1 && a.kv_heads >= 1 && a.q_heads % a.kv_heads == 0, LS_ERR_SHAPE,
+           "%s: query heads must be a positive multiple of KV heads", what);
+  LS_CHECK(a.q_heads / a.kv_heads <= 16, LS_ERR_SHAPE, "%s: at most 16 query heads per KV head", what);
+  LS_CHECK(a.softmax_scale > 0.f && a.softcap >= 0.f, LS_ERR_VALUE, "%s: softmax_scale must be > 0, softcap >= 0",
+           what);
+  if (a.batch == 0) return LS_OK;
+  LS_CHECK(a.query && a.global_keys && a.global_values && a.state_slots && a.local_keys && a.local_values &&
+               a.local_mask && a.raw_output && a.raw_lse && a.output,
+           LS_ERR_VALUE, "%s: every tensor is required", what);
+  LS_CHECK(aligned16(a.query) && aligned16(a.global_keys) && aligned16(a.local_keys) && aligned16(a.output) &&
+               (reinterpret_cast<uintptr_t>(a.raw_output) & 7u) == 0 && a.q_stride_b % 8 == 0 &&
+               a.q_stride_h % 8 == 0 && a.q_stride_r % 8 == 0 && a.gk_stride_b % 8 == 0 &&
+               a.gk_stride_h % 8 == 0 && a.gk_stride_g % 8 == 0 && a.lk_stride_b % 8 == 0 &&
+               a.lk_stride_h % 8 == 0 && a.lk_stride_l % 8 == 0 && a.ro_stride_t % 4 == 0 &&
+               a.ro_stride_h % 4 == 0 && a.o_stride_b % 4 == 0 && a.o_stride_h % 4 == 0 && a.o_stride_r % 4 == 0,
+           LS_ERR_ALIGN, "%s: 16-bit rows must be 16-byte aligned (window and output rows 8-byte aligned)", what);
+  const int64_t grid = a.batch * a.kv_heads;
+  LS_CHECK(grid < (int64_t(1) << 31), LS_ERR_SHAPE, "%s: grid too large", what);
+  const int threads = (a.q_heads / a.kv_heads) * kWave;
+  draft_merge_kernel<<<dim3(static_cast<unsigned>(grid)), threads, 0, static_cast<hipStream_t>(stream)>>>(a);
   LS_LAUNCH_CHECK();
   return LS_OK;
 }

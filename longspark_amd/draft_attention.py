@@ -1,12 +1,19 @@
 """Drafter attention over the three refreshed views, on the GPU.
 
-Drop-in for SRT/speculative/global16_raw256_draft_all_attention.py:283-416
-(``can_use_fused_global_local_raw_attention``,
-``fused_global_local_raw_attention``), which SRT/speculative/global16_raw256.py
-imports (:119-128).  One kernel folds, for every request and query head, the
-Raw256 window (read through the page table), the Global16 summary state and
-the Local7 in-block rows, in the reference's order and at its rounding points.
-``SRT`` = ``vendor/sglang/python/sglang/srt``.
+Drop-ins for both forms the reference's drafter uses
+(SRT/speculative/global16_raw256.py:1460-1600 picks one):
+  * one kernel over all sources -- SRT/speculative/
+    global16_raw256_draft_all_attention.py:283-416
+    (``can_use_fused_global_local_raw_attention``,
+    ``fused_global_local_raw_attention``): for every request and query head
+    the Raw256 window (read through the page table), the Global16 summary
+    state and the Local7 in-block rows, folded in the reference's order and
+    at its rounding points;
+  * the merge after a separate window attention (the default) --
+    SRT/speculative/global16_raw256_draft_fused.py:314-479
+    (``can_use_fused_global_local_raw_merge``,
+    ``fused_global_local_raw_merge``).
+``SPEC`` = ``SRT/speculative``, ``SRT`` = ``vendor/sglang/python/sglang/srt``.
 """
 
 from __future__ import annotations
@@ -110,4 +117,82 @@ def fused_global_local_raw_attention(*, query: torch.Tensor, global_keys: torch.
     a.output = output.data_ptr()
     a.o_stride_b, a.o_stride_h, a.o_stride_r = output.stride()[:3]
     _lib.call("ls_draft_attention", ctypes.byref(a), _lib.stream_of(dev))
+    return output
+
+
+def can_use_fused_global_local_raw_merge(*, query: torch.Tensor, global_keys: torch.Tensor,
+                                         global_values: torch.Tensor, state_slots: Optional[torch.Tensor],
+                                         local_keys: torch.Tensor, local_values: torch.Tensor,
+                                         local_attention_mask: torch.Tensor, raw_output: torch.Tensor,
+                                         raw_lse: torch.Tensor, output: torch.Tensor) -> bool:
+    """The merge form's contract (SPEC/global16_raw256_draft_fused.py:314-369)."""
+    batch, heads = (int(query.shape[0]), int(query.shape[1])) if query.ndim == 4 else (0, 0)
+    return bool(
+        query.is_cuda and query.dtype == torch.bfloat16 and query.ndim == 4
+        and tuple(query.shape[2:]) == (QUERY_ROWS, HEAD_DIM)
+        and tuple(global_keys.shape) == (batch, heads, GLOBAL_ROWS, HEAD_DIM)
+        and global_keys.dtype == torch.bfloat16
+        and global_values.is_cuda and global_values.dtype == torch.float32 and global_values.ndim == 4
+        and tuple(global_values.shape[1:]) == (heads, GLOBAL_ROWS, HEAD_DIM)
+        and state_slots is not None and state_slots.is_cuda and state_slots.dtype == torch.int32
+        and tuple(state_slots.shape) == (batch,)
+        and local_keys.shape == local_values.shape and local_keys.ndim == 4 and local_keys.shape[0] == batch
+        and tuple(local_keys.shape[2:]) == (LOCAL_ROWS, HEAD_DIM)
+        and heads % local_keys.shape[1] == 0
+        and local_keys.dtype == query.dtype and local_values.dtype == query.dtype
+        and local_attention_mask.is_cuda and local_attention_mask.dtype == torch.bool
+        and tuple(local_attention_mask.shape) == (batch, QUERY_ROWS, LOCAL_ROWS)
+        and raw_output.is_cuda and raw_output.dtype == query.dtype
+        and tuple(raw_output.shape) == (batch * QUERY_ROWS, heads, HEAD_DIM)
+        and raw_lse.is_cuda and raw_lse.dtype == torch.float32
+        and tuple(raw_lse.shape) == (batch * QUERY_ROWS, heads)
+        and output.is_cuda and output.dtype == query.dtype and output.shape == query.shape
+    )
+
+
+def fused_global_local_raw_merge(*, query: torch.Tensor, global_keys: torch.Tensor, global_values: torch.Tensor,
+                                 state_slots: torch.Tensor, local_keys: torch.Tensor, local_values: torch.Tensor,
+                                 local_attention_mask: torch.Tensor, raw_output: torch.Tensor,
+                                 raw_lse: torch.Tensor, output: torch.Tensor, softmax_scale: float,
+                                 softcap: float = 0.0, validate_contract: bool = True) -> torch.Tensor:
+    """Merge the window attention with the summary and local sources into
+    caller-owned ``output`` (SPEC/global16_raw256_draft_fused.py:417-479).
+    The contract is checked even when ``validate_contract`` is False: the
+    kernel relies on it."""
+    ok = can_use_fused_global_local_raw_merge(
+        query=query, global_keys=global_keys, global_values=global_values, state_slots=state_slots,
+        local_keys=local_keys, local_values=local_values, local_attention_mask=local_attention_mask,
+        raw_output=raw_output, raw_lse=raw_lse, output=output)
+    if not ok:
+        raise ValueError("Global16 fused Draft tensors violate the production contract")
+    dev = _lib.require_cuda(query, global_keys, global_values, state_slots, local_keys, local_values,
+                            local_attention_mask, raw_output, raw_lse, output, what="fused_global_local_raw_merge")
+    for name, t in (("query", query), ("global_keys", global_keys), ("global_values", global_values),
+                    ("local_keys", local_keys), ("local_values", local_values), ("raw_output", raw_output),
+                    ("output", output)):
+        if t.stride(-1) != 1:
+            raise ValueError(f"fused_global_local_raw_merge: {name} needs a contiguous head dimension")
+    a = _lib.DraftAttentionArgs()
+    a.batch, a.q_heads, a.kv_heads = query.shape[0], query.shape[1], local_keys.shape[1]
+    a.softmax_scale, a.softcap = float(softmax_scale), float(softcap or 0.0)
+    a.query = query.data_ptr()
+    a.q_stride_b, a.q_stride_h, a.q_stride_r = query.stride()[:3]
+    a.global_keys = global_keys.data_ptr()
+    a.gk_stride_b, a.gk_stride_h, a.gk_stride_g = global_keys.stride()[:3]
+    a.global_values = global_values.data_ptr()
+    a.gv_stride_b, a.gv_stride_h, a.gv_stride_g = global_values.stride()[:3]
+    a.state_slots = state_slots.data_ptr()
+    a.local_keys = local_keys.data_ptr()
+    a.lk_stride_b, a.lk_stride_h, a.lk_stride_l = local_keys.stride()[:3]
+    a.local_values = local_values.data_ptr()
+    a.lv_stride_b, a.lv_stride_h, a.lv_stride_l = local_values.stride()[:3]
+    a.local_mask = local_attention_mask.data_ptr()
+    a.lm_stride_b, a.lm_stride_r, a.lm_stride_l = local_attention_mask.stride()
+    a.raw_output = raw_output.data_ptr()
+    a.ro_stride_t, a.ro_stride_h = raw_output.stride(0), raw_output.stride(1)
+    a.raw_lse = raw_lse.data_ptr()
+    a.rl_stride_t, a.rl_stride_h = raw_lse.stride()
+    a.output = output.data_ptr()
+    a.o_stride_b, a.o_stride_h, a.o_stride_r = output.stride()[:3]
+    _lib.call("ls_draft_merge", ctypes.byref(a), _lib.stream_of(dev))
     return output

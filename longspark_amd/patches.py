@@ -83,7 +83,10 @@ def replacements() -> Dict[str, Dict[str, object]]:
             "can_use_fused_global_local_raw_attention": draft_attention.can_use_fused_global_local_raw_attention},
         # recent window (SPEC/global16_raw256_draft_fused.py:372-413, engine/draft.py:14-21)
         "sglang.srt.speculative.global16_raw256_draft_fused": {
-            "build_raw256_page_table": kvwindow.build_raw256_page_table},
+            "build_raw256_page_table": kvwindow.build_raw256_page_table,
+            # the default drafter path's merge after its window attention (:314-479)
+            "fused_global_local_raw_merge": draft_attention.fused_global_local_raw_merge,
+            "can_use_fused_global_local_raw_merge": draft_attention.can_use_fused_global_local_raw_merge},
         "longspark.engine.draft": {"ring_page_table": kvwindow.ring_page_table},
         "longspark.engine.state_export": {"gather_selected_kv": _gather_selected_kv_pool},
     }

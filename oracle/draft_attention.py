@@ -78,3 +78,51 @@ def fused_global_local_raw_attention(query, global_keys, global_values, state_sl
             m, z, acc = _step(m, z, acc, s, local_values[b, kvh].float(), visible=vis)
             out[b, h] = (acc / z[:, None]).to(torch.bfloat16)
     return out
+
+
+def fused_global_local_raw_merge(query, global_keys, global_values, state_slots, local_keys, local_values,
+                                 local_attention_mask, raw_output, raw_lse, softmax_scale: float,
+                                 softcap: float = 0.0) -> torch.Tensor:
+    """Merge form, SRT/speculative/global16_raw256_draft_fused.py:138-312:
+    summary and local sources normalised on their own (bf16 weights and
+    values, the weighted sum rounded to bf16, divided by the fp32 sum),
+    scores bf16(q.k) * scale then ``softcap * tanh(s / softcap)``; merged with
+    ``raw_output [B*7, Hq, D]`` / ``raw_lse [B*7, Hq]`` by their LSEs; a row
+    with no visible local row leaves that term out.  bf16 output."""
+    batch, hq, rows, dim = query.shape
+    hkv = local_keys.shape[1]
+    groups = hq // hkv
+
+    def finish(s):
+        s = _bf16(s) * softmax_scale
+        return torch.tanh(s / softcap) * softcap if softcap > 0 else s
+
+    out = torch.empty(batch, hq, rows, dim, dtype=torch.bfloat16)
+    for b in range(batch):
+        slot = int(state_slots[b])
+        vis = local_attention_mask[b].bool()
+        has = vis.any(dim=1)
+        for h in range(hq):
+            kvh = h // groups
+            q = query[b, h].float()
+            s = finish(q @ global_keys[b, h].float().T)
+            gmax = s.max(dim=1).values
+            w = torch.exp(s - gmax[:, None])
+            gz = w.sum(dim=1)
+            g_out = _bf16(_bf16(w) @ _bf16(global_values[slot, h].float())) / gz[:, None]
+            g_lse = gmax + torch.log(gz)
+            s = finish(q @ local_keys[b, kvh].float().T)
+            s = torch.where(vis, s, torch.full_like(s, NEG_INF))
+            safe = torch.where(has, s.max(dim=1).values, torch.zeros(rows))
+            w = torch.where(vis, torch.exp(s - safe[:, None]), torch.zeros_like(s))
+            lz = torch.where(has, w.sum(dim=1), torch.ones(rows))
+            l_out = _bf16(_bf16(w) @ local_values[b, kvh].float()) / lz[:, None]
+            l_lse = torch.where(has, safe + torch.log(lz), torch.full((rows,), NEG_INF))
+            r_lse = raw_lse[b * rows:(b + 1) * rows, h].float()
+            r_out = raw_output[b * rows:(b + 1) * rows, h].float()
+            mm = torch.maximum(r_lse, torch.maximum(g_lse, l_lse))
+            rw, gw = torch.exp(r_lse - mm), torch.exp(g_lse - mm)
+            lw = torch.where(has, torch.exp(l_lse - mm), torch.zeros(rows))
+            merged = (r_out * rw[:, None] + g_out * gw[:, None] + l_out * lw[:, None]) / (rw + gw + lw)[:, None]
+            out[b, h] = merged.to(torch.bfloat16)
+    return out

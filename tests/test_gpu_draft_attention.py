@@ -82,3 +82,43 @@ def test_draft_attention_contract(dev):
         da.fused_global_local_raw_attention(**{**kw, "page_table": pt[:, :128]})
     with pytest.raises(ValueError, match="violate the contract"):
         da.fused_global_local_raw_attention(**{**kw, "local_attention_mask": mask.to(torch.int32)})
+
+
+@pytest.mark.parametrize("hq,hkv,cap", [(32, 8, 0.0), (40, 8, 3.0), (8, 8, 0.0)])
+def test_draft_merge_matches_oracle(dev, hq, hkv, cap):
+    """Merge form: a window attention output and LSE (random here, one row's
+    LSE -inf; the LSE given as a transposed view) merged with the summary and
+    local sources.  Bound 2^-6 * weighted |v| + 2^-7 * |out| + 1e-6: each
+    source's weighted sum and the output are rounded to bf16 on both sides."""
+    q, gk, gv, slots, lk, lv, mask, kc, vc, pt, rl = make(hq + 7 * hkv, hq, hkv)
+    batch = q.shape[0]
+    g = torch.Generator().manual_seed(hq)
+    raw_out = torch.randn(batch * 7, hq, 128, generator=g).to(torch.bfloat16)
+    raw_lse = (2.0 * torch.randn(hq, batch * 7, generator=g)).t()          # [B*7, Hq], strides (1, B*7)
+    raw_lse[1, 0] = float("-inf")
+    scale = 128 ** -0.5
+    args = [q, gk, gv, slots, lk, lv, mask]
+    print(f"draft merge hq={hq} hkv={hkv} cap={cap}", flush=True)
+    out = torch.empty_like(q).to(dev)
+    da.fused_global_local_raw_merge(query=q.to(dev), global_keys=gk.to(dev), global_values=gv.to(dev),
+                                    state_slots=slots.to(dev), local_keys=lk.to(dev), local_values=lv.to(dev),
+                                    local_attention_mask=mask.to(dev), raw_output=raw_out.to(dev),
+                                    raw_lse=raw_lse.to(dev), output=out, softmax_scale=scale, softcap=cap)
+    torch.cuda.synchronize()
+    ref = oda.fused_global_local_raw_merge(*args, raw_out, raw_lse, scale, softcap=cap).double()
+    wabs = oda.fused_global_local_raw_merge(q, gk, gv.abs(), slots, lk, lv.abs(), mask, raw_out.abs(), raw_lse,
+                                            scale, softcap=cap).double()
+    err = (out.cpu().double() - ref).abs()
+    bound = 2.0 ** -6 * wabs + 2.0 ** -7 * ref.abs() + 1e-6
+    assert bool((err <= bound).all()), (float(err.max()), float((err / bound).max()))
+
+
+def test_draft_merge_contract(dev):
+    q, gk, gv, slots, lk, lv, mask, *_ = [t.to(dev) for t in make(6, 8, 2, lens=[10, 20])]
+    raw_out = torch.zeros(q.shape[0] * 7, 8, 128, dtype=torch.bfloat16, device=dev)
+    raw_lse = torch.zeros(q.shape[0] * 7, 8, device=dev)
+    kw = dict(query=q, global_keys=gk, global_values=gv, state_slots=slots, local_keys=lk, local_values=lv,
+              local_attention_mask=mask, raw_output=raw_out, raw_lse=raw_lse, output=torch.empty_like(q))
+    assert da.can_use_fused_global_local_raw_merge(**kw)
+    with pytest.raises(ValueError, match="violate the production contract"):
+        da.fused_global_local_raw_merge(**{**kw, "raw_lse": raw_lse.half()}, softmax_scale=0.1)

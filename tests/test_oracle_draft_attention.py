@@ -89,3 +89,51 @@ def test_raw_block_size_only_moves_weight_rounding():
     b = oda.fused_global_local_raw_attention(*args, 0.09, block_n=256).double()
     ref, wabs = concat_reference(*args, 0.09)
     assert bool(((a - b).abs() <= 2.0 ** -7 * wabs + 2.0 ** -7 * ref.abs() + 1e-6).all())
+
+
+def window_attention(q, kc, vc, pt, rl, scale):
+    """Exact (fp64) attention of the query rows over each request's window,
+    token-major [B*7, Hq, D] output and [B*7, Hq] LSE, as the reference's
+    FA3 call returns them."""
+    batch, hq = q.shape[:2]
+    hkv = kc.shape[2]
+    out = torch.zeros(batch * 7, hq, 128, dtype=torch.float64)
+    lse = torch.zeros(batch * 7, hq, dtype=torch.float64)
+    for b in range(batch):
+        locs = pt[b, : int(rl[b])].long()
+        for h in range(hq):
+            k = kc[locs, 0, h // (hq // hkv)].double()
+            v = vc[locs, 0, h // (hq // hkv)].double()
+            s = (q[b, h].double() @ k.T) * scale
+            out[b * 7:(b + 1) * 7, h] = torch.softmax(s, 1) @ v
+            lse[b * 7:(b + 1) * 7, h] = torch.logsumexp(s, 1)
+    return out, lse
+
+
+def test_merge_of_window_attention_equals_one_kernel_form():
+    """Merging an exact window attention with the summary and local sources
+    gives the one-softmax-over-everything output, within the rounding bound
+    (each source's weighted sum and both outputs rounded to bf16)."""
+    q, gk, gv, slots, lk, lv, mask, kc, vc, pt, rl = make(4, lens=(150, 60))
+    scale = 128 ** -0.5
+    raw_out, raw_lse = window_attention(q, kc, vc, pt, rl, scale)
+    got = oda.fused_global_local_raw_merge(q, gk, gv, slots, lk, lv, mask, raw_out.to(torch.bfloat16),
+                                           raw_lse.float(), scale).double()
+    ref, wabs = concat_reference(q, gk, gv, slots, lk, lv, mask, kc, vc, pt, rl, scale)
+    bound = 2.0 ** -7 * wabs + 2.0 ** -7 * ref.abs() + 1e-6
+    assert bool(((got - ref).abs() <= bound).all()), float(((got - ref).abs() / bound).max())
+
+
+def test_merge_softcap_closed_form():
+    """One summary key repeated, no local rows and a window LSE of -inf:
+    the output is the mean of the summary values, whatever the softcap."""
+    q, gk, gv, slots, lk, lv, mask, kc, vc, pt, rl = make(5)
+    gk[:] = gk[:, :, :1]
+    mask[:] = False
+    raw_out = torch.randn(q.shape[0] * 7, q.shape[1], 128).to(torch.bfloat16)
+    raw_lse = torch.full((q.shape[0] * 7, q.shape[1]), float("-inf"))
+    for cap in (0.0, 3.0):
+        got = oda.fused_global_local_raw_merge(q, gk, gv, slots, lk, lv, mask, raw_out, raw_lse, 0.2, softcap=cap)
+        for b in range(q.shape[0]):
+            want = gv[int(slots[b])].to(torch.bfloat16).float().mean(dim=1)
+            assert torch.allclose(got[b].float(), want[:, None, :].expand(-1, 7, -1), rtol=2 ** -6, atol=1e-6)
