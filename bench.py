@@ -709,6 +709,52 @@ class DraftAttention:
                 "sample": f"{b} requests, oracle torch-CPU per (request, query head), median of {n} runs"}
 
 
+class DraftMerge(DraftAttention):
+    """fused_global_local_raw_merge: the merge step after a separate window
+    attention, for the same batch and heads as the one-kernel workload: the
+    window attention's bf16 output [B*7, Hq, 128] and fp32 LSE [B*7, Hq]
+    merged with the 16 summary rows (fp32 state) and 7 local rows per query
+    head."""
+
+    name = "draft_merge"
+    metric = "drafter merge GB/s (algorithmic bytes) at B=128, 32 Hq / 8 Hkv, D 128, window output + Global16 + Local7"
+
+    def __init__(self, dev, batch=128, q_heads=32, kv_heads=8):
+        super().__init__(dev, batch=batch, q_heads=q_heads, kv_heads=kv_heads)
+        g = torch.Generator(device=dev).manual_seed(64)
+        self.kc = self.vc = self.pt = None
+        self.raw_out = torch.randn(batch * 7, q_heads, 128, generator=g, device=dev).to(torch.bfloat16)
+        self.raw_lse = 2.0 * torch.randn(batch * 7, q_heads, generator=g, device=dev)
+        # per query head: query, window output and merged output rows (bf16), window LSE, summary keys (bf16)
+        # and fp32 state; per KV head the local K and V rows; the local mask
+        per_head = 3 * 7 * 128 * 2 + 7 * 4 + 16 * 128 * 2 + 16 * 128 * 4
+        self.bytes = batch * q_heads * per_head + 2 * self.lk.numel() * 2 + self.mask.numel()
+        self.units = self.bytes / 1e9
+        self.kernel = "draft_merge_kernel"
+
+    def step(self):
+        from longspark_amd import draft_attention
+        return draft_attention.fused_global_local_raw_merge(
+            query=self.q, global_keys=self.gk, global_values=self.gv, state_slots=self.slots, local_keys=self.lk,
+            local_values=self.lv, local_attention_mask=self.mask, raw_output=self.raw_out, raw_lse=self.raw_lse,
+            output=self.out, softmax_scale=128 ** -0.5)
+
+    def config(self):
+        return {"workload": f"drafter merge B={self.batch} Hq={self.q_heads} Hkv={self.kv_heads} D=128, "
+                            "window output + LSE merged with Global16 + Local7", "batch": self.batch}
+
+    def cpu_baseline(self, threads):
+        from oracle import draft_attention as oda
+        torch.set_num_threads(threads)
+        b = 8
+        args = [t[:b].cpu() for t in (self.q, self.gk, self.gv)] + [torch.arange(b, dtype=torch.int32)] + \
+               [t[:b].cpu() for t in (self.lk, self.lv, self.mask)] + \
+               [self.raw_out[:7 * b].cpu(), self.raw_lse[:7 * b].cpu()]
+        med, n = time_cpu(lambda: oda.fused_global_local_raw_merge(*args, 128 ** -0.5))
+        return {"value": self.bytes * b / self.batch / med / 1e9, "threads": threads,
+                "sample": f"{b} requests, oracle torch-CPU merge, median of {n} runs"}
+
+
 class FullRound:
     """One verify-and-refresh round at Qwen3-14B geometry: 40 layers, 40 query
     and 8 KV heads, head_dim 128, vocab 151,936, batch 128, block 16, contexts
@@ -879,7 +925,7 @@ class AdjustLogits:
 
 WORKLOADS = {w.name: w for w in (GreedyVerify, StochasticVerify, WindowGather, SummaryUpdate, SoftmaxTempWorkload,
                                   TargetProbsWorkload, ChainSampling, AdjustLogits, SampleStep, Global16Prefill, DraftAttention,
-                                  FullRound, HbmCopy)}
+                                  DraftMerge, FullRound, HbmCopy)}
 DEFAULT_WORKLOAD = "verify_sample"
 
 

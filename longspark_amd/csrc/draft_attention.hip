@@ -45,14 +45,16 @@ constexpr int kDB = kD / 16;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr size_t kLds = static_cast<size_t>(kBlk) * kKP * 2 + static_cast<size_t>(kD) * kVP * 2;
 
-__device__ __forceinline__ float round_bf16(float x) { return to_f32<uint16_t>(from_f32<uint16_t>(x)); }
-
 __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
   typedef __attribute__((ext_vector_type(2))) float f32x2;
   typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
   const f32x2 v = {lo, hi};
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
 }
+
+// x rounded to bf16 (nearest even) and widened back, through the hardware
+// conversion (v_cvt_pk_bf16_f32) rather than integer rounding with a NaN branch.
+__device__ __forceinline__ float round_bf16(float x) { return __builtin_bit_cast(float, pack_bf16(x, 0.f) << 16); }
 
 __device__ __forceinline__ uint32_t half16(const uint4& v, int e) {
   const uint32_t w = e < 2 ? v.x : (e < 4 ? v.y : (e < 6 ? v.z : v.w));
@@ -281,23 +283,6 @@ __global__ __launch_bounds__(1024) void draft_attention_kernel(const ls_draft_at
 // sources are normalised on their own and the three merged by their LSEs.
 // One wave per query head; no LDS.
 
-// Weighted sum of one 16-source tile: O^T[16 d x 16 rows] = V^T . P^T with
-// the bf16 weights w[i] of sources 4*g16 + i (the second 16-source half of
-// the 32-deep product is zero).
-template <typename VT>
-__device__ __forceinline__ void tile_output(f32x4_t (&o)[kDB], const float (&w)[4], VT vt) {
-  uint4 pb;
-  pb.x = pack_bf16(w[0], w[1]);
-  pb.y = pack_bf16(w[2], w[3]);
-  pb.z = 0u;
-  pb.w = 0u;
-#pragma unroll
-  for (int db = 0; db < kDB; ++db) {
-    const uint2 lo = vt(db);
-    o[db] = Mma<BF16>::run(make_uint4(lo.x, lo.y, 0u, 0u), pb, f32x4_t{0.f, 0.f, 0.f, 0.f});
-  }
-}
-
 __device__ __forceinline__ float row_max4(float v) {
   v = fmaxf(v, __shfl_xor(v, 16, kWave));
   return fmaxf(v, __shfl_xor(v, 32, kWave));
@@ -307,7 +292,10 @@ __device__ __forceinline__ float row_sum4(float v) {
   return v + __shfl_xor(v, 32, kWave);
 }
 
-__global__ __launch_bounds__(1024) void draft_merge_kernel(const ls_draft_attention_args a) {
+// kMaxThreads bounds the workgroup (64 x query heads per KV head); the
+// smaller bounds leave the compiler registers for the loads issued up front.
+template <int kMaxThreads>
+__global__ __launch_bounds__(kMaxThreads) void draft_merge_kernel(const ls_draft_attention_args a) {
   const int64_t b = blockIdx.x / a.kv_heads;
   const int kvh = static_cast<int>(blockIdx.x % a.kv_heads);
   const int groups = a.q_heads / a.kv_heads;
@@ -315,6 +303,7 @@ __global__ __launch_bounds__(1024) void draft_merge_kernel(const ls_draft_attent
   const int g16 = lane >> 4, c16 = lane & 15;
   const int head = kvh * groups + wave;
   const bool row_ok = c16 < kRows;
+  const int row = row_ok ? c16 : 0;   // lanes past the 7 query rows read row 0 and store nothing
   const float cap = a.softcap;
   auto finish = [&](float t) __attribute__((always_inline)) {
     float s = round_bf16(t) * a.softmax_scale;
@@ -322,77 +311,115 @@ __global__ __launch_bounds__(1024) void draft_merge_kernel(const ls_draft_attent
     return s;
   };
 
-  uint4 qb[kKB];
+  // Every load of the wave is issued here, before any of them is used, so
+  // the wave waits for one memory round trip (plus the state slot) instead
+  // of one per source.
+  const int64_t tok = b * kRows + row;
+  const float rlse = a.raw_lse[tok * a.rl_stride_t + head * a.rl_stride_h];
+  uint2 rov[kDB];
+  {
+    const uint16_t* ro = static_cast<const uint16_t*>(a.raw_output) + tok * a.ro_stride_t + head * a.ro_stride_h;
+#pragma unroll
+    for (int db = 0; db < kDB; ++db) rov[db] = *reinterpret_cast<const uint2*>(ro + db * 16 + 4 * g16);
+  }
+  uint4 qb[kKB], gkb[kKB], lkb[kKB];
   {
     const uint16_t* q = static_cast<const uint16_t*>(a.query) + b * a.q_stride_b + head * a.q_stride_h +
-                        (row_ok ? c16 : 0) * a.q_stride_r;
+                        row * a.q_stride_r;
+    const uint16_t* gk = static_cast<const uint16_t*>(a.global_keys) + b * a.gk_stride_b + head * a.gk_stride_h +
+                         c16 * a.gk_stride_g;
+    const uint16_t* lk = static_cast<const uint16_t*>(a.local_keys) + b * a.lk_stride_b + kvh * a.lk_stride_h +
+                         (c16 < kLocal ? c16 : 0) * a.lk_stride_l;
 #pragma unroll
     for (int kb = 0; kb < kKB; ++kb) {
-      const uint4 v = load16(q + kb * 32 + g16 * 8);
-      qb[kb] = row_ok ? v : make_uint4(0u, 0u, 0u, 0u);
+      qb[kb] = load16(q + kb * 32 + g16 * 8);
+      gkb[kb] = load16(gk + kb * 32 + g16 * 8);
+      lkb[kb] = load16(lk + kb * 32 + g16 * 8);
     }
+  }
+  // local values of sources 4*g16 .. 4*g16+3 (those past the 7 rows are 0), column db*16 + c16, as bf16 pairs
+  uint32_t lvp[kDB][2];
+  {
+    const uint16_t* lv = static_cast<const uint16_t*>(a.local_values) + b * a.lv_stride_b + kvh * a.lv_stride_h;
+#pragma unroll
+    for (int db = 0; db < kDB; ++db) {
+      uint32_t h[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        // unconditional load of a clamped row, then a select (no branch per load)
+        const int src = 4 * g16 + e;
+        const uint32_t v = lv[(src < kLocal ? src : kLocal - 1) * a.lv_stride_l + db * 16 + c16];
+        h[e] = src < kLocal ? v : 0u;
+      }
+      lvp[db][0] = h[0] | (h[1] << 16);
+      lvp[db][1] = h[2] | (h[3] << 16);
+    }
+  }
+  bool vis[4];
+  {
+    const uint8_t* mrow = a.local_mask + b * a.lm_stride_b + row * a.lm_stride_r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int src = 4 * g16 + i;
+      vis[i] = row_ok && src < kLocal && mrow[(src < kLocal ? src : 0) * a.lm_stride_l] != 0;
+    }
+  }
+  // summary state rows 4*g16 .. 4*g16+3, column db*16 + c16 (fp32, rounded to bf16 as they are packed)
+  float gvr[kDB][4];
+  {
+    const int64_t slot = a.state_slots[b];
+    const float* gv = a.global_values + slot * a.gv_stride_b + head * a.gv_stride_h + (4 * g16) * a.gv_stride_g + c16;
+#pragma unroll
+    for (int db = 0; db < kDB; ++db)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) gvr[db][i] = gv[i * a.gv_stride_g + db * 16];
+  }
+  if (!row_ok) {
+    // q rows past 7 take part in no product's output row, but the tile
+    // products below read every lane's query operand: give them zeros
+#pragma unroll
+    for (int kb = 0; kb < kKB; ++kb) qb[kb] = make_uint4(0u, 0u, 0u, 0u);
+  }
+
+  // Both score tiles first, so the key and query operands are dead before
+  // the value products need their registers.
+  f32x4_t gacc = {0.f, 0.f, 0.f, 0.f}, lacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int kb = 0; kb < kKB; ++kb) {
+    gacc = Mma<BF16>::run(gkb[kb], qb[kb], gacc);
+    lacc = Mma<BF16>::run(c16 < kLocal ? lkb[kb] : make_uint4(0u, 0u, 0u, 0u), qb[kb], lacc);
   }
 
   // ---- global: normalised over its 16 rows ----
-  f32x4_t go[kDB];
-  float glse;
+  float gw4[4], gz, glse;
   {
-    const uint16_t* gk = static_cast<const uint16_t*>(a.global_keys) + b * a.gk_stride_b + head * a.gk_stride_h +
-                         c16 * a.gk_stride_g;
-    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int kb = 0; kb < kKB; ++kb) acc = Mma<BF16>::run(load16(gk + kb * 32 + g16 * 8), qb[kb], acc);
-    float sc[4], w[4];
+    float sc[4];
     float mx = -__builtin_inff();
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      sc[i] = finish(acc[i]);
+      sc[i] = finish(gacc[i]);
       mx = fmaxf(mx, sc[i]);
     }
     mx = row_max4(mx);
     float z = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      w[i] = expf(sc[i] - mx);
-      z += w[i];
+      gw4[i] = expf(sc[i] - mx);
+      z += gw4[i];
     }
-    z = row_sum4(z);
-    const int64_t slot = a.state_slots[b];
-    const float* gv = a.global_values + slot * a.gv_stride_b + head * a.gv_stride_h;
-    tile_output(go, w, [&](int db) __attribute__((always_inline)) {
-      const float* col = gv + (4 * g16) * a.gv_stride_g + db * 16 + c16;
-      return make_uint2(pack_bf16(col[0], col[a.gv_stride_g]),
-                        pack_bf16(col[2 * a.gv_stride_g], col[3 * a.gv_stride_g]));
-    });
-#pragma unroll
-    for (int db = 0; db < kDB; ++db)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) go[db][i] = round_bf16(go[db][i]) / z;
-    glse = mx + logf(z);
+    gz = row_sum4(z);
+    glse = mx + logf(gz);
   }
 
   // ---- local: normalised over its visible rows (none: left out) ----
-  f32x4_t lo[kDB];
-  float llse;
+  float lw4[4], lz, llse;
   bool has;
   {
-    const uint16_t* lk = static_cast<const uint16_t*>(a.local_keys) + b * a.lk_stride_b + kvh * a.lk_stride_h +
-                         (c16 < kLocal ? c16 : 0) * a.lk_stride_l;
-    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int kb = 0; kb < kKB; ++kb) {
-      const uint4 v = load16(lk + kb * 32 + g16 * 8);
-      acc = Mma<BF16>::run(c16 < kLocal ? v : make_uint4(0u, 0u, 0u, 0u), qb[kb], acc);
-    }
-    const uint8_t* mrow = a.local_mask + b * a.lm_stride_b + (row_ok ? c16 : 0) * a.lm_stride_r;
-    bool vis[4];
-    float sc[4], w[4];
+    float sc[4];
     float mx = -__builtin_inff(), nvis = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int src = 4 * g16 + i;
-      vis[i] = row_ok && src < kLocal && mrow[(src < kLocal ? src : 0) * a.lm_stride_l] != 0;
-      sc[i] = vis[i] ? finish(acc[i]) : -__builtin_inff();
+      sc[i] = vis[i] ? finish(lacc[i]) : -__builtin_inff();
       mx = fmaxf(mx, sc[i]);
       nvis += vis[i] ? 1.f : 0.f;
     }
@@ -402,48 +429,40 @@ __global__ __launch_bounds__(1024) void draft_merge_kernel(const ls_draft_attent
     float z = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      w[i] = vis[i] ? expf(sc[i] - safe) : 0.f;
-      z += w[i];
+      lw4[i] = vis[i] ? expf(sc[i] - safe) : 0.f;
+      z += lw4[i];
     }
     z = row_sum4(z);
-    const float safe_z = has ? z : 1.f;
-    const uint16_t* lv = static_cast<const uint16_t*>(a.local_values) + b * a.lv_stride_b + kvh * a.lv_stride_h;
-    tile_output(lo, w, [&](int db) __attribute__((always_inline)) {
-      uint32_t h[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int src = 4 * g16 + e;
-        h[e] = src < kLocal ? lv[src * a.lv_stride_l + db * 16 + c16] : 0u;
-      }
-      return make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
-    });
-#pragma unroll
-    for (int db = 0; db < kDB; ++db)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) lo[db][i] = round_bf16(lo[db][i]) / safe_z;
-    llse = has ? safe + logf(safe_z) : -__builtin_inff();
+    lz = has ? z : 1.f;
+    llse = has ? safe + logf(lz) : -__builtin_inff();
   }
 
-  // ---- merge with the window attention by LSE ----
-  if (!row_ok) return;
-  const int64_t tok = b * kRows + c16;
-  const float rlse = a.raw_lse[tok * a.rl_stride_t + head * a.rl_stride_h];
+  // ---- merge with the window attention by LSE, one 16-column block at a time ----
   const float mm = fmaxf(rlse, fmaxf(glse, llse));
   const float rw = expf(rlse - mm), gw = expf(glse - mm), lw = has ? expf(llse - mm) : 0.f;
   const float norm = rw + gw + lw;
-  const uint16_t* ro = static_cast<const uint16_t*>(a.raw_output) + tok * a.ro_stride_t + head * a.ro_stride_h;
-  uint16_t* out = static_cast<uint16_t*>(a.output) + b * a.o_stride_b + head * a.o_stride_h + c16 * a.o_stride_r;
+  // weights of sources 4*g16 .. 4*g16+3 as the B operand (the second 16-source half of the 32-deep product is 0)
+  const uint4 gpb = make_uint4(pack_bf16(gw4[0], gw4[1]), pack_bf16(gw4[2], gw4[3]), 0u, 0u);
+  const uint4 lpb = make_uint4(pack_bf16(lw4[0], lw4[1]), pack_bf16(lw4[2], lw4[3]), 0u, 0u);
+  // one reciprocal per normaliser: x * (1/z) is within one fp32 ulp of x / z, far inside the bf16 output
+  const float inv_gz = 1.f / gz, inv_lz = 1.f / lz, inv_norm = 1.f / norm;
+  uint16_t* out = static_cast<uint16_t*>(a.output) + b * a.o_stride_b + head * a.o_stride_h + row * a.o_stride_r;
 #pragma unroll
   for (int db = 0; db < kDB; ++db) {
-    const uint2 rv = *reinterpret_cast<const uint2*>(ro + db * 16 + 4 * g16);
-    float r4[4] = {bf16_lo(rv.x), bf16_hi(rv.x), bf16_lo(rv.y), bf16_hi(rv.y)};
+    const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
+    const f32x4_t go = Mma<BF16>::run(
+        make_uint4(pack_bf16(gvr[db][0], gvr[db][1]), pack_bf16(gvr[db][2], gvr[db][3]), 0u, 0u), gpb, zero);
+    const f32x4_t lo = Mma<BF16>::run(make_uint4(lvp[db][0], lvp[db][1], 0u, 0u), lpb, zero);
+    const uint2 rv = rov[db];
+    const float r4[4] = {bf16_lo(rv.x), bf16_hi(rv.x), bf16_lo(rv.y), bf16_hi(rv.y)};
     float y[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) y[i] = (r4[i] * rw + go[db][i] * gw + lo[db][i] * lw) / norm;
+    for (int i = 0; i < 4; ++i)
+      y[i] = (r4[i] * rw + (round_bf16(go[i]) * inv_gz) * gw + (round_bf16(lo[i]) * inv_lz) * lw) * inv_norm;
     uint2 w;
     w.x = pack_bf16(y[0], y[1]);
     w.y = pack_bf16(y[2], y[3]);
-    *reinterpret_cast<uint2*>(out + db * 16 + 4 * g16) = w;
+    if (row_ok) *reinterpret_cast<uint2*>(out + db * 16 + 4 * g16) = w;
   }
 }
 
@@ -505,7 +524,14 @@ extern "C" int ls_draft_merge(const ls_draft_attention_args* args, void* stream)
   const int64_t grid = a.batch * a.kv_heads;
   LS_CHECK(grid < (int64_t(1) << 31), LS_ERR_SHAPE, "%s: grid too large", what);
   const int threads = (a.q_heads / a.kv_heads) * kWave;
-  draft_merge_kernel<<<dim3(static_cast<unsigned>(grid)), threads, 0, static_cast<hipStream_t>(stream)>>>(a);
+  const dim3 g(static_cast<unsigned>(grid));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (threads <= 256)
+    draft_merge_kernel<256><<<g, threads, 0, st>>>(a);
+  else if (threads <= 512)
+    draft_merge_kernel<512><<<g, threads, 0, st>>>(a);
+  else
+    draft_merge_kernel<1024><<<g, threads, 0, st>>>(a);
   LS_LAUNCH_CHECK();
   return LS_OK;
 }
