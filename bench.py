@@ -88,6 +88,8 @@ def time_cpu(fn, *, warmup=3, reps=20, budget_s=30.0):
 class GreedyVerify:
     """Greedy chain verification, batch 128 x block 16 x vocab 151,936 bf16."""
 
+    copies, rotate = 2, ("logits", "cand")
+
     name = "verify_greedy"
 
     def __init__(self, dev, batch=128, width=16, vocab=V):
@@ -161,6 +163,8 @@ class StochasticVerify:
     temperature 0.7, top-k 50, top-p 0.95, repetition 1.05 over a 2048-token
     Zipf(1.1) history; draft rows fp32; one penalty-table build + one fused
     verify per step."""
+
+    copies, rotate = 2, ("d",)
 
     name = "verify_sample"
 
@@ -260,13 +264,19 @@ class WindowGather:
     The pool holds 8 x 131,072 tokens per layer (K and V, 154.6 GB) with the
     pages of every request placed by one random permutation; only the pages
     the window touches are filled (N(0,1) bf16) -- the rest is allocated but
-    never read, so filling it would only lengthen the set-up."""
+    never read, so filling it would only lengthen the set-up.
+
+    Consecutive steps rotate over ``rotate`` disjoint windows (contexts
+    131,072, 130,816, ... one window apart) and as many output views, so one
+    rotation reads 4 x 302 MB: more than the 256 MB last-level cache, and no
+    step finds the previous step's rows in it."""
 
     name = "kv_window_gather"
     metric = "recent-window gather GB/s (algorithmic bytes) at 36L x 8 Hkv x D128, ps 16, B 8, ctx 131072"
     unit = "GB/s"
 
-    def __init__(self, dev, batch=8, layers=36, heads=8, dim=128, page_size=16, context=131072, window=256):
+    def __init__(self, dev, batch=8, layers=36, heads=8, dim=128, page_size=16, context=131072, window=256,
+                 rotate=4):
         self.dev, self.batch, self.layers, self.heads, self.dim = dev, batch, layers, heads, dim
         self.page_size, self.context, self.window = page_size, context, window
         g = torch.Generator(device=dev).manual_seed(31)
@@ -274,29 +284,37 @@ class WindowGather:
         total_pages = batch * pages_per
         perm = torch.randperm(total_pages, generator=g, device=dev).to(torch.int32)
         self.table = perm.view(batch, pages_per)
-        self.seq_lens = torch.full((batch,), context, dtype=torch.int64, device=dev)
+        self.seq_sets = [torch.full((batch,), context - j * window, dtype=torch.int64, device=dev)
+                         for j in range(rotate)]
+        self.seq_lens = self.seq_sets[0]
         n = total_pages * page_size
         self.k = [torch.empty(n, heads, dim, dtype=torch.bfloat16, device=dev) for _ in range(layers)]
         self.v = [torch.empty(n, heads, dim, dtype=torch.bfloat16, device=dev) for _ in range(layers)]
-        first = (context - window) // page_size
+        first = (context - rotate * window) // page_size
         touched = self.table[:, first:].reshape(-1).long()
         rows = (touched[:, None] * page_size + torch.arange(page_size, device=dev)[None, :]).reshape(-1)
         for t in self.k + self.v:
             t[rows] = torch.randn(rows.numel(), heads, dim, generator=g, device=dev).to(torch.bfloat16)
-        self.out = torch.empty(batch, layers, 2, heads, window, dim, dtype=torch.bfloat16, device=dev)
+        self.outs = [torch.empty(batch, layers, 2, heads, window, dim, dtype=torch.bfloat16, device=dev)
+                     for _ in range(rotate)]
+        self.out = self.outs[0]
+        self.turn = 0
         self.bytes = 2 * self.out.numel() * 2          # every window row read once and written once
         self.kernel = "window_gather_kernel"
         self.units = self.bytes / 1e9
 
     def step(self):
         from longspark_amd import kvwindow
-        return kvwindow.gather_window(self.k, self.v, self.table, self.seq_lens, page_size=self.page_size,
-                                      window=self.window, out=self.out)
+        i = self.turn % len(self.outs)
+        self.turn += 1
+        return kvwindow.gather_window(self.k, self.v, self.table, self.seq_sets[i], page_size=self.page_size,
+                                      window=self.window, out=self.outs[i])
 
     def config(self):
         return {"workload": f"recent-window gather B={self.batch} L={self.layers} Hkv={self.heads} D={self.dim} "
                             f"page size {self.page_size}, context {self.context}, window {self.window}, bf16, "
-                            "random page permutation", "batch": self.batch}
+                            f"random page permutation, {len(self.outs)} disjoint windows in rotation",
+                "batch": self.batch}
 
     def cpu_baseline(self, threads):
         from oracle import kvwindow as okw
@@ -319,6 +337,8 @@ class SummaryUpdate:
     """Fused summary update (scores + merge, all layers in one launch), Qwen3-8B
     geometry: 36 layers, 32 query heads x 64 rows (256 rows per KV head), 8 KV
     heads, head_dim 128, 16 new rows per request (all accepted), batch 8."""
+
+    copies, rotate = 2, ("state", "lse")
 
     name = "summary_update"
     dtype = "f32"
@@ -494,6 +514,8 @@ class ChainSampling:
     draft [B, K-1, V] probabilities (softmax of N(0, 3^2) logits at T 0.8,
     drafted tokens drawn from q), batch 128 x block 16."""
 
+    copies, rotate = 7, ("p", "q")
+
     name = "chain_sampling"
     metric = "dense-q chain sampling GB/s (algorithmic bytes) at 128x16x151936 fp32 probabilities"
     unit = "GB/s"
@@ -556,6 +578,8 @@ class SampleStep:
     """sample_step_tokens_with_q: the drafter's per-step exponential race with
     the sampled q over fp32 logits [128, 151,936] and fp32 Exp(1) noise of the
     same shape (one proposal step of a batch of 128)."""
+
+    copies, rotate = 7, ("logits", "noise")
 
     name = "sample_step"
     metric = "proposal-step sampling GB/s (algorithmic bytes) at 128x151936 fp32 logits + fp32 noise"
@@ -658,6 +682,8 @@ class DraftAttention:
     rows per query head from the fp32 state, 7 local rows under a causal
     in-block mask."""
 
+    copies, rotate = 5, ("q", "gk", "gv", "lk", "lv", "mask", "kc", "vc", "pt", "out")
+
     name = "draft_attention"
     metric = "drafter attention GB/s (algorithmic bytes) at B=128, 32 Hq / 8 Hkv, D 128, Raw256 + Global16 + Local7"
     unit = "GB/s"
@@ -716,6 +742,8 @@ class DraftMerge(DraftAttention):
     window attention's bf16 output [B*7, Hq, 128] and fp32 LSE [B*7, Hq]
     merged with the 16 summary rows (fp32 state) and 7 local rows per query
     head."""
+
+    copies, rotate = 13, ("q", "gk", "gv", "lk", "lv", "mask", "raw_out", "raw_lse", "out")
 
     name = "draft_merge"
     metric = "drafter merge GB/s (algorithmic bytes) at B=128, 32 Hq / 8 Hkv, D 128, window output + Global16 + Local7"
@@ -879,6 +907,8 @@ class AdjustLogits:
     acc_linear_penalties and logit_bias [B, V] added in bf16 to every row of
     each request, in place on [B*K, V] bf16 logits, batch 128 x block 16."""
 
+    copies, rotate = 2, ("logits",)
+
     name = "adjust_logits"
     metric = "verify logit adjustments GB/s (algorithmic bytes) at 128x16x151936 bf16"
     unit = "GB/s"
@@ -930,6 +960,40 @@ WORKLOADS = {w.name: w for w in (GreedyVerify, StochasticVerify, WindowGather, S
 DEFAULT_WORKLOAD = "verify_sample"
 
 
+def _clone(x):
+    if torch.is_tensor(x):
+        return x.clone()
+    if isinstance(x, dict):
+        return {k: _clone(v) for k, v in x.items()}
+    if isinstance(x, list):
+        return [_clone(v) for v in x]
+    return x
+
+
+class Rotation:
+    """Input rotation: a workload whose tensors fit in the 256 MB last-level
+    cache (or come close) names them in ``rotate``; ``copies`` - 1 clones go
+    to distinct memory and consecutive steps use the copies in turn, so one
+    cycle touches at least about 1 GB and no step re-reads lines an earlier
+    step left in the cache.  The copies hold equal values, so every step
+    computes the same result."""
+
+    def __init__(self, wl):
+        self.wl = wl
+        names = getattr(wl, "rotate", ())
+        n = getattr(wl, "copies", 1) if names else 1
+        self.sets = [{k: getattr(wl, k) for k in names}]
+        self.sets += [{k: _clone(getattr(wl, k)) for k in names} for _ in range(n - 1)]
+        self.turn = 0
+
+    def step(self):
+        if len(self.sets) > 1:
+            for k, v in self.sets[self.turn % len(self.sets)].items():
+                setattr(self.wl, k, v)
+            self.turn += 1
+        return self.wl.step()
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -950,13 +1014,14 @@ def main(argv=None):
     torch.cuda.set_device(dev)
     wl = WORKLOADS[args.workload](dev)
     stream = torch.cuda.current_stream(dev)
+    rot = Rotation(wl)
 
     out = None
     for _ in range(args.warmup):
-        out = wl.step()
+        out = rot.step()
     torch.cuda.synchronize()
     if hasattr(wl, "count_rejected"):
-        wl.count_rejected(out if out is not None else wl.step())
+        wl.count_rejected(out if out is not None else rot.step())
     if hasattr(wl, "arm_timing"):
         wl.arm_timing(args.steps)
     start = torch.cuda.Event(enable_timing=True)
@@ -964,7 +1029,7 @@ def main(argv=None):
     t0 = time.perf_counter()
     start.record(stream)
     for _ in range(args.steps):
-        wl.step()
+        rot.step()
     end.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
@@ -1000,7 +1065,7 @@ def main(argv=None):
         "vs_baseline": None,
         "dtype": getattr(wl, "dtype", "bf16"),
         "data": "synthetic",
-        "config": wl.config(),
+        "config": {**wl.config(), "input_copies": len(rot.sets)},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": TRAFFIC.get(wl.kernel, (None,))[0],
                      "traffic_source": TRAFFIC.get(wl.kernel, (None, None))[1], "kernel": wl.kernel,
