@@ -168,11 +168,13 @@ class StochasticVerify:
 
     name = "verify_sample"
 
+    boost_drafted = False
+
     def __init__(self, dev, batch=128, width=16, vocab=V):
         from longspark_amd import workloads
         self.dev, self.batch, self.width, self.vocab = dev, batch, width, vocab
-        self.cfg = dict(temperature=0.7, top_k=50, top_p=0.95, history_len=2048, repetition=1.05)
-        self.d = workloads.stochastic_inputs(batch, width, vocab, seed=2025, device=dev, gen_device=dev, **self.cfg)
+        self.cfg = dict(workloads.VERIFY_BENCH_CFG)
+        self.d = workloads.verify_bench_inputs(dev, batch, width, vocab, boost_drafted=self.boost_drafted)
         self.rows = batch * width
         # The dominant kernel scans every target row and, in the same launch, the
         # fp32 draft row at the rejection of every request that rejects a token.
@@ -190,6 +192,7 @@ class StochasticVerify:
         accept = out[0]
         rejected = int((accept < self.width - 1).sum().item())
         self.rejected = rejected
+        self.mean_accepted = float(accept.float().mean().item())
         self.kernel_bytes = self.rows * self.vocab * 2 + rejected * self.vocab * 4
 
     # One timed step in TIMING_EVERY records the four HIP events of the C ABI
@@ -231,10 +234,14 @@ class StochasticVerify:
                 "resolve_kernel": resolve}
 
     def config(self):
+        where = ("+8 on the drafted token with probability 0.7 (applied after drafting)" if self.boost_drafted
+                 else "+8 on uniform random candidates (replaced by the tokens drawn from q)")
         return {"workload": f"fused stochastic verify B={self.batch} K={self.width} V={self.vocab} bf16, T 0.7, "
-                            "top-k 50, top-p 0.95, repetition 1.05 over a 2048-token Zipf history; draft rows fp32",
+                            "top-k 50, top-p 0.95, repetition 1.05 over a 2048-token Zipf history; draft rows fp32; "
+                            f"target boost {where}",
                 "batch": self.batch, "block": self.width, "vocab": self.vocab,
-                "rejecting_requests": getattr(self, "rejected", None)}
+                "rejecting_requests": getattr(self, "rejected", None),
+                "mean_accepted": getattr(self, "mean_accepted", None)}
 
     def cpu_baseline(self, threads):
         from oracle import verify as ov
@@ -257,6 +264,17 @@ class StochasticVerify:
                           f"(penalties, target distribution, acceptance, residual draw), median of {n} runs"}
 
 
+class StochasticVerifyHighAccept(StochasticVerify):
+    """The fused stochastic verify of ``verify_sample`` with the +8 target
+    boost on the drafted tokens (probability 0.7 per position, applied after
+    drafting): requests accept long prefixes and reject late, so the draft
+    slices wait on later target rows and some requests draw their bonus from
+    the last target row."""
+
+    name = "verify_sample_high_accept"
+    boost_drafted = True
+
+
 class WindowGather:
     """Recent-window gather, Qwen3-8B geometry: 36 layers, 8 KV heads, head_dim
     128, page size 16, batch 8 at a 131,072-token context (window 256).
@@ -277,24 +295,13 @@ class WindowGather:
 
     def __init__(self, dev, batch=8, layers=36, heads=8, dim=128, page_size=16, context=131072, window=256,
                  rotate=4):
+        from longspark_amd import workloads
         self.dev, self.batch, self.layers, self.heads, self.dim = dev, batch, layers, heads, dim
         self.page_size, self.context, self.window = page_size, context, window
-        g = torch.Generator(device=dev).manual_seed(31)
-        pages_per = context // page_size
-        total_pages = batch * pages_per
-        perm = torch.randperm(total_pages, generator=g, device=dev).to(torch.int32)
-        self.table = perm.view(batch, pages_per)
-        self.seq_sets = [torch.full((batch,), context - j * window, dtype=torch.int64, device=dev)
-                         for j in range(rotate)]
+        w = workloads.window_pool(dev, batch=batch, layers=layers, heads=heads, dim=dim, page_size=page_size,
+                                  context=context, window=window, rotate=rotate)
+        self.k, self.v, self.table, self.seq_sets = w["k"], w["v"], w["table"], w["seq_sets"]
         self.seq_lens = self.seq_sets[0]
-        n = total_pages * page_size
-        self.k = [torch.empty(n, heads, dim, dtype=torch.bfloat16, device=dev) for _ in range(layers)]
-        self.v = [torch.empty(n, heads, dim, dtype=torch.bfloat16, device=dev) for _ in range(layers)]
-        first = (context - rotate * window) // page_size
-        touched = self.table[:, first:].reshape(-1).long()
-        rows = (touched[:, None] * page_size + torch.arange(page_size, device=dev)[None, :]).reshape(-1)
-        for t in self.k + self.v:
-            t[rows] = torch.randn(rows.numel(), heads, dim, generator=g, device=dev).to(torch.bfloat16)
         self.outs = [torch.empty(batch, layers, 2, heads, window, dim, dtype=torch.bfloat16, device=dev)
                      for _ in range(rotate)]
         self.out = self.outs[0]
@@ -807,26 +814,12 @@ class FullRound:
         self.verify = StochasticVerify(dev, batch=batch, width=width)
         self.batch, self.width, self.layers, self.dim, self.window, self.page = batch, width, layers, dim, window, page
         self.q_heads, self.kv_heads, self.rows = q_heads, kv_heads, rows
-        g = torch.Generator(device=dev).manual_seed(91)
-        ctx = torch.randint(8192, 32769, (batch,), generator=g, device=dev)
-        pages_per = 32768 // page
-        win_pages = window // page + 1
-        pool_pages = 2 * batch * win_pages
-        table = torch.randint(0, pool_pages, (batch, pages_per), generator=g, device=dev, dtype=torch.int32)
-        own = torch.randperm(pool_pages, generator=g, device=dev)[:batch * win_pages].view(batch, win_pages)
-        cols = ((ctx - window) // page)[:, None] + torch.arange(win_pages, device=dev)[None, :]
-        table.scatter_(1, cols.clamp(max=pages_per - 1), own.to(torch.int32))
-        self.table, self.seq = table, ctx
-        n = pool_pages * page
-        self.k = [torch.randn(n, kv_heads, dim, generator=g, device=dev).to(torch.bfloat16) for _ in range(layers)]
-        self.v = [torch.randn(n, kv_heads, dim, generator=g, device=dev).to(torch.bfloat16) for _ in range(layers)]
+        from longspark_amd import workloads
+        r = workloads.full_round_refresh_inputs(dev, batch=batch, width=width, layers=layers, q_heads=q_heads,
+                                                kv_heads=kv_heads, dim=dim, rows=rows, page=page, window=window)
+        self.table, self.seq, self.k, self.v, self.locs = r["table"], r["seq"], r["k"], r["v"], r["locs"]
+        self.query, self.state, self.lse = r["query"], r["state"], r["lse"]
         self.out = torch.empty(batch, layers, 2, kv_heads, window, dim, dtype=torch.bfloat16, device=dev)
-        # committed rows: the last `width` positions of each context
-        pos = ctx[:, None] - width + torch.arange(width, device=dev)[None, :]
-        self.locs = table.gather(1, (pos // page)).long() * page + pos % page
-        self.query = torch.randn(layers, q_heads, rows, dim, generator=g, device=dev).to(torch.bfloat16)
-        self.state = torch.randn(batch, layers, q_heads, rows, dim, generator=g, device=dev)
-        self.lse = torch.randn(batch, layers, q_heads, rows, generator=g, device=dev)
         self.committed = width * batch
         self._set_bytes(self.verify.rows * V * 2 + batch * V * 4)
         self.kernel = "full round (all kernels of the round)"
@@ -954,7 +947,7 @@ class AdjustLogits:
                 "threads": threads, "sample": f"{b} requests, torch-CPU adds of the reference, median of {n} runs"}
 
 
-WORKLOADS = {w.name: w for w in (GreedyVerify, StochasticVerify, WindowGather, SummaryUpdate, SoftmaxTempWorkload,
+WORKLOADS = {w.name: w for w in (GreedyVerify, StochasticVerify, StochasticVerifyHighAccept, WindowGather, SummaryUpdate, SoftmaxTempWorkload,
                                   TargetProbsWorkload, ChainSampling, AdjustLogits, SampleStep, Global16Prefill, DraftAttention,
                                   DraftMerge, FullRound, HbmCopy)}
 DEFAULT_WORKLOAD = "verify_sample"

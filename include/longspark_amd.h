@@ -136,9 +136,8 @@ LS_API int ls_penalty_tables(const int32_t* history, int64_t history_stride, con
  * (apply_dflash_verify_logits_adjustments: verify_quirk = 1 builds the bias
  * on a zero tensor as that function does, verify_quirk = 0 applies the
  * penalties to the logits themselves in the order of
- * SRT/sampling/sampling_batch_info.py:269-286) and, with no penalty tables,
- * SRT/constrained/triton_ops/bitmask_ops.py:84-141
- * (apply_token_bitmask_inplace_triton).
+ * SRT/sampling/sampling_batch_info.py:269-286).  The bitmask alone, with
+ * row indices, is ls_apply_token_bitmask below.
  * rows_per_request: rows of one request (penalty table b = row / rows_per_request);
  * mask_rows_per_request: 1 (one mask row per logits row) or rows_per_request
  * (one mask row per request).  Arithmetic is fp32; bf16/fp16 rows are rounded
@@ -169,6 +168,28 @@ LS_API int ls_add_request_bias(void* logits, int32_t logits_dtype, int64_t row_s
                                int32_t rows_per_request, const float* bias, int64_t bias_stride,
                                const int32_t* vocab_mask, int64_t mask_stride, int64_t mask_words,
                                const float* bias2, int64_t bias2_stride, int32_t separate, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Vocabulary (grammar) bitmask applied in place: replaces
+ * SRT/constrained/triton_ops/bitmask_ops.py:84-141
+ * (apply_token_bitmask_inplace_triton(logits, bitmask, indices)) and the
+ * ROCm binding the grammar backend calls instead,
+ * sgl_kernel.apply_token_bitmask_inplace_cuda (SRT/constrained/
+ * xgrammar_backend.py:43-48,112-117,239-244).
+ * logits [logits_rows, vocab] (fp32/bf16/fp16, row stride row_stride);
+ * bitmask int32 [mask_rows, mask_words] (row stride mask_stride), LSB first:
+ * bit (v & 31) of word v >> 5 equal to 0 sets logits[row, v] = -inf, for
+ * v < min(vocab, 32 * mask_words); other columns are untouched.
+ * mask_words <= ceil(vocab / 32) (the reference's width check).
+ * indices (int32 or int64 [num_rows], may be NULL): the rows to mask; index i
+ * selects both logits row i and bitmask row i (bitmask_ops.py:61-64).  An
+ * index outside either tensor is skipped.  Without indices rows 0 ..
+ * num_rows-1 are masked.
+ * ------------------------------------------------------------------------- */
+LS_API int ls_apply_token_bitmask(void* logits, int32_t logits_dtype, int64_t row_stride, int64_t logits_rows,
+                                  int64_t vocab, const int32_t* bitmask, int64_t mask_stride, int64_t mask_rows,
+                                  int64_t mask_words, const void* indices, int32_t indices_dtype, int64_t num_rows,
+                                  void* stream);
 
 /* ---------------------------------------------------------------------------
  * Fused stochastic chain verification of a drafted block.

@@ -151,6 +151,7 @@ _SIGNATURES = {
     "ls_penalty_tables": (I32, [P, I64, P, I64, I32, I64, P, P, P, P, I64, P, I64, P, P, P]),
     "ls_adjust_logits": (I32, [P, I32, I64, I64, I64, I32, P, P, I64, P, I64, P, I32, P, I64, I32, I64, P]),
     "ls_add_request_bias": (I32, [P, I32, I64, I64, I64, I32, P, I64, P, I64, I64, P, I64, I32, P]),
+    "ls_apply_token_bitmask": (I32, [P, I32, I64, I64, I64, P, I64, I64, I64, P, I32, I64, P]),
     "ls_verify_sample_workspace": (I32, [I64, I32, I64, I32, P, P]),
     "ls_verify_sample": (I32, [ctypes.POINTER(VerifySampleArgs), P, U64, P, U64, P]),
     "ls_softmax_temp": (I32, [P, I32, I64, I64, I64, P, I32, P, I64, P]),
@@ -224,6 +225,11 @@ def stream_of(device: torch.device):
     return torch.cuda.current_stream(device).cuda_stream
 
 
+def capturing() -> bool:
+    """True while torch's current stream is recording a HIP graph."""
+    return torch.cuda.is_available() and torch.cuda.is_current_stream_capturing()
+
+
 def require_cuda(*tensors, what: str) -> torch.device:
     """All given (non-None) tensors must live on one GPU; returns that device."""
     dev = None
@@ -253,16 +259,23 @@ class _Workspaces:
 
     The counter buffer is zero-filled when (re)allocated and every C ABI call
     leaves it zero, so one buffer serves every entry point on a stream.
-    Buffers only grow; growing reallocates (zero-filled for counters).
+    Buffers only grow; growing allocates a larger buffer (zero-filled for
+    counters) and keeps the old one alive until the process ends, because a
+    HIP graph captured earlier may still launch kernels that use it.  Run
+    each op once on the capture stream before capturing (torch's usual
+    warm-up), so that capture finds its buffers already sized.
     """
 
     def __init__(self):
         self._bufs = {}
+        self._retired = []
 
     def _get(self, kind: str, nbytes: int, device: torch.device) -> torch.Tensor:
         key = (kind, device.index, stream_of(device))
         buf = self._bufs.get(key)
         if buf is None or buf.numel() < nbytes:
+            if buf is not None:
+                self._retired.append(buf)
             n = max(int(nbytes), 4096)
             buf = torch.zeros(n, dtype=torch.uint8, device=device) if kind == "counters" else \
                 torch.empty(n, dtype=torch.uint8, device=device)

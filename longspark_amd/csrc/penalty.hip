@@ -215,6 +215,68 @@ __global__ __launch_bounds__(kRB) void request_bias_kernel(
   }
 }
 
+// Vocabulary bitmask in place (the grammar mask): bit (v & 31) of word
+// v >> 5 of the row's mask, LSB first; a 0 bit sets the logit to -inf.  One
+// thread owns one mask word, i.e. 32 consecutive columns.  A word with every
+// bit set changes nothing and is skipped without touching the logits; any
+// other word's columns are read as 16-byte vectors, the masked ones replaced,
+// and written back whole (4 vectors for 16-bit logits, 8 for fp32), so a
+// wavefront moves 4 or 8 KiB of contiguous logits per access.  Rows come
+// from `indices` when given (the same index selects the logits row and the
+// mask row); an index outside either tensor is skipped.
+template <typename T>
+__device__ __forceinline__ T neg_inf_bits();
+template <>
+__device__ __forceinline__ float neg_inf_bits<float>() { return -INFINITY; }
+template <>
+__device__ __forceinline__ uint16_t neg_inf_bits<uint16_t>() { return 0xff80u; }
+template <>
+__device__ __forceinline__ __half neg_inf_bits<__half>() { return __ushort_as_half(0xfc00u); }
+
+constexpr int kBM = 256;
+
+template <typename T, bool kVec>
+__global__ __launch_bounds__(kBM) void token_bitmask_kernel(T* __restrict__ logits, int64_t row_stride,
+                                                            int64_t logits_rows, int64_t mvocab,
+                                                            const uint32_t* __restrict__ mask, int64_t mask_stride,
+                                                            int64_t mask_rows, const void* __restrict__ indices,
+                                                            int idx_i64, int64_t num_rows) {
+  const int64_t w = static_cast<int64_t>(blockIdx.x) * kBM + threadIdx.x;
+  const int64_t words = (mvocab + 31) >> 5;
+  if (w >= words) return;
+  for (int64_t r = blockIdx.y; r < num_rows; r += gridDim.y) {
+    const int64_t row = !indices ? r
+                        : idx_i64 ? static_cast<const int64_t*>(indices)[r]
+                                  : static_cast<int64_t>(static_cast<const int32_t*>(indices)[r]);
+    if (row < 0 || row >= logits_rows || row >= mask_rows) continue;
+    const uint32_t bits = mask[row * mask_stride + w];
+    if (bits == 0xffffffffu) continue;
+    T* p = logits + row * row_stride + w * 32;
+    const int64_t n = mvocab - w * 32 < 32 ? mvocab - w * 32 : 32;
+    if (kVec && n == 32) {
+      constexpr int kPer = 16 / sizeof(T);  // elements per 16-byte vector
+      constexpr int kN = 32 / kPer;
+      union U {
+        uint4 v;
+        T e[kPer];
+      } u[kN];
+      uint4* vp = reinterpret_cast<uint4*>(p);
+#pragma unroll
+      for (int i = 0; i < kN; ++i) u[i].v = vp[i];
+#pragma unroll
+      for (int i = 0; i < kN; ++i)
+#pragma unroll
+        for (int e = 0; e < kPer; ++e)
+          if (!((bits >> (i * kPer + e)) & 1u)) u[i].e[e] = neg_inf_bits<T>();
+#pragma unroll
+      for (int i = 0; i < kN; ++i) vp[i] = u[i].v;
+    } else {
+      for (int e = 0; e < n; ++e)
+        if (!((bits >> e) & 1u)) p[e] = neg_inf_bits<T>();
+    }
+  }
+}
+
 }  // namespace
 }  // namespace ls
 
@@ -313,6 +375,52 @@ extern "C" int ls_add_request_bias(void* logits, int32_t logits_dtype, int64_t r
   else if (logits_dtype == LS_F16) LS_RB(__half);
   else return fail(LS_ERR_DTYPE, "ls_add_request_bias: logits must be fp32, bf16 or fp16");
 #undef LS_RB
+  LS_LAUNCH_CHECK();
+  return LS_OK;
+}
+
+extern "C" int ls_apply_token_bitmask(void* logits, int32_t logits_dtype, int64_t row_stride, int64_t logits_rows,
+                                      int64_t vocab, const int32_t* bitmask, int64_t mask_stride, int64_t mask_rows,
+                                      int64_t mask_words, const void* indices, int32_t indices_dtype,
+                                      int64_t num_rows, void* stream) {
+  using namespace ls;
+  LS_CHECK(logits && bitmask, LS_ERR_VALUE, "ls_apply_token_bitmask: null logits or bitmask");
+  LS_CHECK(logits_rows > 0 && vocab > 0 && row_stride >= vocab, LS_ERR_SHAPE,
+           "ls_apply_token_bitmask: need logits_rows > 0, vocab > 0, row_stride >= vocab");
+  LS_CHECK(mask_rows > 0 && mask_words > 0 && mask_stride >= mask_words, LS_ERR_SHAPE,
+           "ls_apply_token_bitmask: bad bitmask shape");
+  LS_CHECK(mask_words <= (vocab + 31) / 32, LS_ERR_SHAPE,
+           "ls_apply_token_bitmask: bitmask width %lld exceeds ceil(vocab / 32) = %lld", (long long)mask_words,
+           (long long)((vocab + 31) / 32));
+  LS_CHECK(!indices || indices_dtype == LS_I32 || indices_dtype == LS_I64, LS_ERR_DTYPE,
+           "ls_apply_token_bitmask: indices must be int32 or int64");
+  LS_CHECK(num_rows >= 0, LS_ERR_SHAPE, "ls_apply_token_bitmask: negative row count");
+  LS_CHECK(indices || (num_rows <= logits_rows && num_rows <= mask_rows), LS_ERR_SHAPE,
+           "ls_apply_token_bitmask: more rows than the logits or the bitmask hold");
+  if (num_rows == 0) return LS_OK;
+  const int64_t mvocab = mask_words * 32 < vocab ? mask_words * 32 : vocab;
+  const int64_t words = (mvocab + 31) / 32;
+  const dim3 grid(static_cast<unsigned>((words + kBM - 1) / kBM),
+                  static_cast<unsigned>(num_rows < 65535 ? num_rows : 65535));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const uint32_t* m = reinterpret_cast<const uint32_t*>(bitmask);
+  const int i64 = indices_dtype == LS_I64 ? 1 : 0;
+#define LS_BM(T)                                                                                              \
+  do {                                                                                                        \
+    T* lp = static_cast<T*>(logits);                                                                          \
+    const bool vec = aligned16(lp) && (row_stride * static_cast<int64_t>(sizeof(T))) % 16 == 0;                \
+    if (vec)                                                                                                  \
+      token_bitmask_kernel<T, true><<<grid, kBM, 0, s>>>(lp, row_stride, logits_rows, mvocab, m, mask_stride,  \
+                                                          mask_rows, indices, i64, num_rows);                   \
+    else                                                                                                      \
+      token_bitmask_kernel<T, false><<<grid, kBM, 0, s>>>(lp, row_stride, logits_rows, mvocab, m, mask_stride, \
+                                                           mask_rows, indices, i64, num_rows);                  \
+  } while (0)
+  if (logits_dtype == LS_F32) LS_BM(float);
+  else if (logits_dtype == LS_BF16) LS_BM(uint16_t);
+  else if (logits_dtype == LS_F16) LS_BM(__half);
+  else return fail(LS_ERR_DTYPE, "ls_apply_token_bitmask: logits must be fp32, bf16 or fp16");
+#undef LS_BM
   LS_LAUNCH_CHECK();
   return LS_OK;
 }

@@ -19,6 +19,9 @@ Drop-ins for both forms the reference's drafter uses
 from __future__ import annotations
 
 import ctypes
+import json
+import os
+import warnings
 from typing import Optional
 
 import torch
@@ -67,6 +70,31 @@ def can_use_fused_global_local_raw_attention(*, query: torch.Tensor, global_keys
     )
 
 
+RAW_BLOCK = 64  # window rows per online-softmax step (the reference's default block)
+_warned_blocks = set()
+
+
+def _configured_raw_block(batch: int) -> int:
+    """The window block the reference would use for this batch: entry
+    ``[block, warps, stages]`` of ``DFK_GLOBAL16_DRAFT_ATTENTION_CONFIGS``
+    (a JSON object keyed by batch size or "default"), else 64
+    (SPEC/global16_raw256_draft_all_attention.py:20-46, same validation and
+    messages).  Warps and stages are launch choices with no effect on the
+    result; the block sets where the online softmax rescales and where the
+    weights are rounded to bf16."""
+    raw = os.getenv("DFK_GLOBAL16_DRAFT_ATTENTION_CONFIGS", "{}")
+    table = json.loads(raw)
+    if not isinstance(table, dict):
+        raise ValueError("Draft attention launch configurations must be a JSON object")
+    for key, config in table.items():
+        if key != "default" and (not key.isdecimal() or int(key) < 1):
+            raise ValueError("Draft attention batch keys must be positive integers or default")
+        if (not isinstance(config, list) or len(config) != 3 or config[0] not in (32, 64, 128)
+                or config[1] not in (4, 8) or config[2] not in (1, 2, 3)):
+            raise ValueError("Unsupported Draft attention launch configuration")
+    return int(table.get(str(batch), table.get("default", [RAW_BLOCK]))[0])
+
+
 def fused_global_local_raw_attention(*, query: torch.Tensor, global_keys: torch.Tensor, global_values: torch.Tensor,
                                      state_slots: torch.Tensor, local_keys: torch.Tensor, local_values: torch.Tensor,
                                      local_attention_mask: torch.Tensor, key_cache: torch.Tensor,
@@ -76,6 +104,15 @@ def fused_global_local_raw_attention(*, query: torch.Tensor, global_keys: torch.
     (draft_all_attention.py:348-416, same checks and messages)."""
     if float(softcap) != 0.0:
         raise ValueError("fused all-source Draft attention requires softcap=0")
+    block = _configured_raw_block(int(query.shape[0]))
+    if block != RAW_BLOCK and block not in _warned_blocks:
+        # This kernel always steps the window in blocks of 64 rows, the
+        # reference's default; another block moves the result only within the
+        # bf16 weight-rounding bound.
+        _warned_blocks.add(block)
+        warnings.warn(f"DFK_GLOBAL16_DRAFT_ATTENTION_CONFIGS selects a {block}-row window block; the gfx950 "
+                      f"drafter attention steps the window in blocks of {RAW_BLOCK} rows (the reference default), "
+                      "so results match that configuration", RuntimeWarning, stacklevel=2)
     if not can_use_fused_global_local_raw_attention(
             query=query, global_keys=global_keys, global_values=global_values, state_slots=state_slots,
             local_keys=local_keys, local_values=local_values, local_attention_mask=local_attention_mask,

@@ -12,6 +12,7 @@ src/longspark/engine/draft.py:207-212, 255-259).  ``SRT`` =
 
 from __future__ import annotations
 
+import weakref
 from typing import Optional, Sequence, Union
 
 import torch
@@ -24,32 +25,81 @@ _INDEX = (torch.int32, torch.int64)
 
 
 class LayerPointers:
-    """Device arrays of per-layer base addresses, cached by the addresses.
+    """Device arrays of per-layer base addresses, one per live set of layer tensors.
 
     KV pools keep one tensor per layer; the kernels take a device array of
     their base addresses.  The array is built once per distinct set of layer
     tensors (a small host-to-device copy) and reused afterwards.
+
+    An array lives exactly as long as the tensors it points into: each entry
+    holds weak references to the storage owners of its layers (the tensor a
+    view was taken from), and only entries whose owners have all been freed
+    are dropped.  A HIP graph that captured a launch therefore never sees its
+    pointer array freed while the pool it points into is alive.
+
+    A host-to-device copy cannot be recorded into a graph, so the first use of
+    a pool must come before capture: call :meth:`prepare` (or any op on the
+    pool) first.  A lookup during capture that finds no array raises.
     """
 
-    def __init__(self, limit: int = 64):
+    def __init__(self, sweep_every: int = 64):
         self._cache = {}
-        self._limit = limit
+        self._sweep_every = sweep_every
+        self._built = 0
+
+    @staticmethod
+    def _addresses(layers: Layers):
+        if isinstance(layers, torch.Tensor):
+            return tuple(layers.data_ptr() + i * layers.stride(0) * layers.element_size()
+                         for i in range(layers.shape[0])), (layers,)
+        items = list(layers)
+        return tuple(t.data_ptr() for t in items), items
+
+    @staticmethod
+    def _owner(t: torch.Tensor) -> torch.Tensor:
+        while t._base is not None:
+            t = t._base
+        return t
+
+    def _sweep(self):
+        dead = [k for k, (arr, refs) in self._cache.items() if any(r() is None for r in refs)]
+        for k in dead:
+            del self._cache[k]
 
     def get(self, layers: Layers, device: torch.device) -> torch.Tensor:
-        if isinstance(layers, torch.Tensor):
-            addrs = tuple(layers.data_ptr() + i * layers.stride(0) * layers.element_size()
-                          for i in range(layers.shape[0]))
-        else:
-            addrs = tuple(t.data_ptr() for t in layers)
-        key = (device.index, addrs)
-        arr = self._cache.get(key)
-        if arr is None:
-            if len(self._cache) >= self._limit:
-                self._cache.clear()
-            arr = torch.tensor([a if a < 1 << 63 else a - (1 << 64) for a in addrs], dtype=torch.int64,
-                               device=device)
-            self._cache[key] = arr
+        addrs, items = self._addresses(layers)
+        key = (getattr(device, "index", None), addrs)
+        hit = self._cache.get(key)
+        if hit is not None and all(r() is not None for r in hit[1]):
+            return hit[0]
+        if self._capturing():
+            raise RuntimeError("KV layer pointer array built during graph capture: call "
+                               "longspark_amd.kvwindow.layer_pointers.prepare(layers) before capturing")
+        self._built += 1
+        if self._built % self._sweep_every == 0:
+            self._sweep()
+        owners = {id(o): o for o in (self._owner(t) for t in items)}
+        refs = tuple(weakref.ref(o) for o in owners.values())
+        arr = self._make_array(addrs, device)
+        self._cache[key] = (arr, refs)
         return arr
+
+    @staticmethod
+    def _capturing() -> bool:
+        return _lib.capturing()
+
+    @staticmethod
+    def _make_array(addrs, device) -> torch.Tensor:
+        return torch.tensor([a if a < 1 << 63 else a - (1 << 64) for a in addrs], dtype=torch.int64, device=device)
+
+    def prepare(self, *layer_sets: Layers) -> None:
+        """Build the pointer arrays of the given pools now (before a graph capture)."""
+        for layers in layer_sets:
+            items = list(layers) if not isinstance(layers, torch.Tensor) else [layers]
+            self.get(layers, items[0].device)
+
+    def __len__(self):
+        return len(self._cache)
 
 
 layer_pointers = LayerPointers()

@@ -64,14 +64,30 @@ def replacements() -> Dict[str, Dict[str, object]]:
         # committed verify rows into req_to_token (SPEC/draft_free_kv_info.py:32-82)
         "sglang.srt.speculative.draft_free_kv_info": {
             "_assign_fixed_verify_cache_locs_func": verify.assign_fixed_verify_cache_locs},
-        # vocabulary bitmask (SRT/constrained/triton_ops/bitmask_ops.py:84-141)
+        # vocabulary bitmask (SRT/constrained/triton_ops/bitmask_ops.py:84-141), and the grammar
+        # backend's own bindings: it imports the Triton function, or on ROCm
+        # sgl_kernel.apply_token_bitmask_inplace_cuda, by name at import time
+        # (SRT/constrained/xgrammar_backend.py:43-48) and calls them at :112-117 and :239-244
         "sglang.srt.constrained.triton_ops.bitmask_ops": {
             "apply_token_bitmask_inplace_triton": penalties.apply_token_bitmask_inplace},
+        "sglang.srt.constrained.xgrammar_backend": {
+            "apply_token_bitmask_inplace_triton": penalties.apply_token_bitmask_inplace,
+            "apply_token_bitmask_inplace_cuda": penalties.apply_token_bitmask_inplace},
         # summary state (SPEC/global16_raw256_incremental.py:400-584; the GQA-5
         # adapter's wrappers are covered by the same functions)
         "sglang.srt.speculative.global16_raw256_incremental": {
             "cache_position_scores": summary.cache_position_scores,
             "merge_accepted_positions_": summary.merge_accepted_positions_},
+        # the Qwen3-14B GQA-5 adapter (src/longspark/patches/gqa5_attention.py): its install()
+        # (:109-112) rebinds the two functions above to its module-level wrappers and, for other
+        # group sizes, those wrappers fall back to the functions it captured at import (:13-14).
+        # Replacing all four names makes a later gqa5_attention.install() bind these ops again,
+        # whichever of the two installs runs first.
+        "longspark.patches.gqa5_attention": {
+            "cache_position_scores": summary.cache_position_scores,
+            "merge_accepted_positions_": summary.merge_accepted_positions_,
+            "_original_scores": summary.cache_position_scores,
+            "_original_merge": summary.merge_accepted_positions_},
         # prefill summary initialisation (SPEC/global16_raw256.py:668-784), a method of the
         # verify context class: dotted names replace a class attribute
         "sglang.srt.speculative.global16_raw256": {

@@ -7,7 +7,7 @@ logit-adjustment call sites).
 from __future__ import annotations
 
 from dataclasses import dataclass
-from typing import Optional
+from typing import List, Optional, Union
 
 import torch
 
@@ -106,19 +106,40 @@ def adjust_logits_(logits: torch.Tensor, *, rows_per_request: int, tables: Optio
               vocab_mask.shape[1] if vocab_mask is not None else 0, _lib.stream_of(dev))
 
 
-def apply_token_bitmask_inplace(logits: torch.Tensor, bitmask: torch.Tensor) -> None:
-    """SRT/constrained/triton_ops/bitmask_ops.py:84-141 (without ``indices``):
-    bit 0 of ``bitmask[row, v >> 5] >> (v & 31)`` sets ``-inf``; only the first
-    ``min(V, 32 * W)`` columns are touched."""
+def apply_token_bitmask_inplace(logits: torch.Tensor, bitmask: torch.Tensor,
+                                indices: Optional[Union[List[int], torch.Tensor]] = None) -> None:
+    """SRT/constrained/triton_ops/bitmask_ops.py:84-141 (``apply_token_bitmask_inplace_triton``)
+    and the ROCm binding ``sgl_kernel.apply_token_bitmask_inplace_cuda`` that
+    SRT/constrained/xgrammar_backend.py:43-48 calls instead: bit 0 of
+    ``bitmask[row, v >> 5] >> (v & 31)`` sets ``logits[row, v] = -inf`` for
+    ``v < min(V, 32 * W)``; other columns are untouched.  ``indices`` (a list
+    or tensor) selects the rows; the same index selects the logits row and
+    the bitmask row.  The checks and their messages are the reference's
+    assertions."""
+    assert bitmask.dtype == torch.int32, "bitmask must be of type int32"
     if logits.ndim == 1:
         logits = logits.unsqueeze(0)
     if bitmask.ndim == 1:
         bitmask = bitmask.unsqueeze(0)
-    if bitmask.shape[1] > (logits.shape[1] + 31) // 32:
-        raise ValueError("bitmask width too large for the logits width")
-    if bitmask.shape[0] != logits.shape[0]:
-        raise ValueError("batch size mismatch between logits and bitmask")
-    adjust_logits_(logits, rows_per_request=1, vocab_mask=bitmask)
+    required = (logits.shape[1] + 31) // 32
+    assert required >= bitmask.shape[1], (
+        f"Bitmask width too large: allow at most {required} int32s for logits' width {logits.shape[1]}, "
+        f"but got {bitmask.shape[1]}")
+    dev = _lib.require_cuda(logits, bitmask, what="apply_token_bitmask_inplace")
+    if isinstance(indices, (list, torch.Tensor)):
+        idx = torch.as_tensor(indices, dtype=torch.int32, device=dev).reshape(-1).contiguous()
+        num_rows = idx.shape[0]
+    else:
+        assert logits.shape[0] == bitmask.shape[0], (
+            f"batch size mismatch: logits {logits.shape[0]} vs bitmask {bitmask.shape[0]}")
+        idx, num_rows = None, logits.shape[0]
+    if logits.stride(-1) != 1 or bitmask.stride(-1) != 1:
+        raise ValueError("apply_token_bitmask_inplace: logits and bitmask rows must be contiguous")
+    if num_rows == 0 or logits.shape[0] == 0 or bitmask.shape[1] == 0:
+        return
+    _lib.call("ls_apply_token_bitmask", logits.data_ptr(), _lib.dtype_code(logits), logits.stride(0),
+              logits.shape[0], logits.shape[1], bitmask.data_ptr(), bitmask.stride(0), bitmask.shape[0],
+              bitmask.shape[1], _lib.ptr(idx), _lib.LS_I32, num_rows, _lib.stream_of(dev))
 
 
 def _request_rows(t: Optional[torch.Tensor], batch: int, vocab: int, what: str, name: str):

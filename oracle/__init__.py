@@ -19,5 +19,6 @@ Modules:
               top-k / top-p / min-p target distributions, penalties, bitmask.
   summary  -- Global16 position scores, online-softmax merge, full-prefix state.
   kvwindow -- Raw256 page table, recent-window gather, ring append.
-  synth    -- seeded synthetic inputs for the benchmark workloads.
+  draft_attention -- the drafter's attention over the window, summary and
+              local views (one-kernel form and merge form).
 """

@@ -21,45 +21,49 @@ import torch
 
 
 def position_scores(global_query: torch.Tensor, new_keys: torch.Tensor, softmax_scale: float,
-                    softcap: float = 0.0) -> torch.Tensor:
+                    softcap: float = 0.0, dtype=torch.float32) -> torch.Tensor:
     """``[B, Hq, S, D]`` x ``[B, W, Hkv, D]`` -> ``[B, Hq, S, W]`` fp32 scores.
 
     global16_raw256_incremental.py:76-87: fp32 einsum over D, times the scale,
     then ``softcap * tanh(s / softcap)`` when softcap > 0 (:44-47).
+    ``dtype=torch.float64`` evaluates the same formula in fp64 (ground truth
+    for tolerance checks).
     """
     batch, hq, rows, dim = global_query.shape
     w, hkv = new_keys.shape[1], new_keys.shape[2]
     groups = hq // hkv
-    q = global_query.float().reshape(batch, hkv, groups, rows, dim)
-    k = new_keys.float().permute(0, 2, 1, 3)
+    q = global_query.to(dtype).reshape(batch, hkv, groups, rows, dim)
+    k = new_keys.to(dtype).permute(0, 2, 1, 3)
     scores = torch.einsum("bhgrd,bhwd->bhgrw", q, k) * float(softmax_scale)
     if softcap > 0:
         scores = torch.tanh(scores / softcap) * softcap
     return scores.reshape(batch, hq, rows, w)
 
 
-def merge_accepted_positions(state_output, state_lse, position_scores_, accepted_values, accept_lens):
+def merge_accepted_positions(state_output, state_lse, position_scores_, accepted_values, accept_lens,
+                             dtype=torch.float32):
     """Online-softmax merge of the first ``accept_lens[b]`` rows into (output, lse).
 
     global16_raw256_incremental.py:124-166 restated with W = ``accepted_values.shape[1]``:
     masked scores, ``merged = logsumexp(stack(lse, logsumexp(scores)))``,
     ``out = out * exp(lse - merged) + sum_w exp(s_w - merged) * v_w``.
+    ``dtype=torch.float64`` evaluates the same formula in fp64.
     """
     batch, hq, rows, dim = state_output.shape
     w = accepted_values.shape[1]
     hkv = accepted_values.shape[2]
     positions = torch.arange(w, dtype=accept_lens.dtype)
     valid = positions[None, :] < accept_lens[:, None]
-    masked = position_scores_.float().masked_fill(~valid[:, None, None, :], float("-inf"))
-    merged_lse = torch.logsumexp(torch.stack((state_lse.float(), torch.logsumexp(masked, dim=-1))), dim=0)
-    prior_weight = torch.exp(state_lse.float() - merged_lse)
+    masked = position_scores_.to(dtype).masked_fill(~valid[:, None, None, :], float("-inf"))
+    merged_lse = torch.logsumexp(torch.stack((state_lse.to(dtype), torch.logsumexp(masked, dim=-1))), dim=0)
+    prior_weight = torch.exp(state_lse.to(dtype) - merged_lse)
     delta_weight = torch.exp(masked - merged_lse[..., None])
     delta_weight = torch.where(valid[:, None, None, :], delta_weight, torch.zeros_like(delta_weight))
     groups = hq // hkv
     weights = delta_weight.view(batch, hkv, groups, rows, w)
-    values = accepted_values.float().permute(0, 2, 1, 3)
+    values = accepted_values.to(dtype).permute(0, 2, 1, 3)
     delta_out = torch.einsum("bhgrw,bhwd->bhgrd", weights, values).reshape(batch, hq, rows, dim)
-    return state_output.float() * prior_weight[..., None] + delta_out, merged_lse
+    return state_output.to(dtype) * prior_weight[..., None] + delta_out, merged_lse
 
 
 def full_prefix_state(global_query, keys, values, softmax_scale: float, dtype=torch.float64, softcap: float = 0.0):

@@ -122,3 +122,33 @@ def test_assign_fixed_verify_cache_locs(dev, idx_dtype):
                                           verify_cache_locs=locs.to(dev), batch_size=bs, verify_width=width)
     torch.cuda.synchronize()
     assert torch.equal(got.cpu(), want)
+
+
+def test_split_hand_cases(dev):
+    """The hand-worked cases of tests/split_cases.py through the GPU path."""
+    from tests import split_cases as sc
+    p, cand, q, u, exp = sc.decide_case()
+    for cdt in (torch.int32, torch.int64):
+        d = verify.decide_acceptance(candidates=cand.to(cdt).to(dev), sampled_q=q.to(dev), target_probs=p.to(dev),
+                                     uniforms=u.to(dev))
+        torch.cuda.synchronize()
+        assert d.lengths.cpu().tolist() == exp["lengths"]
+        assert d.rejected_rows.cpu().tolist() == exp["rejected_rows"]
+        assert d.rejection_positions.cpu().tolist() == exp["rejection_positions"]
+        for b, j in enumerate(exp["target_row_index"]):
+            assert torch.equal(d.target_rows[b].cpu(), p[b, j]), b
+        q_rows, uf, expected = sc.finish_case()
+        assert verify.finish_sampling(d, q_rows.to(dev), uniforms=uf.to(dev)).cpu().tolist() == expected
+    cases, (clamp_row, u_clamp, tok_clamp) = sc.threshold_cases()
+    one = lambda x: torch.tensor(x, device=dev)  # noqa: E731
+    for label, p_row, q_row, ufin, tok in cases:
+        pp = torch.stack([p_row, p_row])[None].to(dev)
+        d = verify.decide_acceptance(candidates=one([[0]]), sampled_q=one([[1.0]]), target_probs=pp,
+                                     uniforms=one([[0.5]]))
+        assert verify.finish_sampling(d, q_row[None].to(dev), uniforms=one([ufin])).cpu().tolist() == [tok], label
+    pp = torch.stack([torch.tensor([0.0, 1.0, 0.0, 0.0]), clamp_row])[None].to(dev)
+    d = verify.decide_acceptance(candidates=one([[1]]), sampled_q=one([[0.5]]), target_probs=pp,
+                                 uniforms=one([[0.5]]))
+    assert d.lengths.cpu().tolist() == [1]
+    tok = verify.finish_sampling(d, torch.zeros(0, 4, device=dev), uniforms=one([u_clamp])).cpu().tolist()
+    assert tok == [tok_clamp]

@@ -1,5 +1,9 @@
-"""Summary state refresh on the GPU vs the CPU oracle (fp32, 2e-5 / 3e-5 as in
-the reference's own GQA-5 test, tests/gpu/test_gqa5_attention.py:21-50).
+"""Summary state refresh on the GPU vs the CPU oracle.
+
+Tolerances: scores within 2e-5 (the reference's own GQA-5 test,
+tests/gpu/test_gqa5_attention.py:21-50, which is re-created here with its
+tolerances); summary entries within 1e-5 relative of the oracle evaluated in
+fp64 (tests/summary_ref.py states what "relative" means for a weighted sum).
 
 Cases: the reference test re-created (seed 980426, batch 1 / 3 / 64, 40 query
 heads over 8 KV heads, 16 rows, 8 new rows, 16 steps, strided state views,
@@ -16,10 +20,11 @@ import torch
 
 from oracle import summary as osm
 from longspark_amd import summary
+from tests import summary_ref as sr
 
 pytestmark = pytest.mark.gpu
 
-TOL = dict(rtol=3e-5, atol=3e-5)
+REF_TOL = dict(rtol=3e-5, atol=3e-5)  # tests/gpu/test_gqa5_attention.py:49-50
 
 
 @pytest.mark.parametrize("q_heads", [40, 32])
@@ -33,6 +38,7 @@ def test_reference_gqa_test_recreated(dev, q_heads):
         lse_base = torch.randn(capacity, 2, q_heads, 16, generator=g)
         slots = torch.randperm(capacity, generator=g)[:batch].to(torch.int32)
         exp_out, exp_lse = out_base[:, 1][slots.long()].clone(), lse_base[:, 1][slots.long()].clone()
+        x_out, x_lse, x_mag = exp_out.double(), exp_lse.double(), exp_out.double().abs()
         out_d, lse_d = out_base.to(dev), lse_base.to(dev)
         output, lse = out_d[:, 1], lse_d[:, 1]
         qd = query.to(dev)
@@ -47,13 +53,18 @@ def test_reference_gqa_test_recreated(dev, q_heads):
             lens = ((torch.arange(batch) + step) % 8 + 1).to(torch.int32)
             locs = torch.arange(batch * 8).reshape(batch, 8)
             exp_out, exp_lse = osm.merge_accepted_positions(exp_out, exp_lse, ref_scores, values, lens)
+            x_out, x_lse, x_mag = sr.merged(x_out, x_lse, x_mag, query, keys, values, lens, 128 ** -.5)
             summary.merge_accepted_positions_(state_output=output, state_lse=lse, position_scores=scores,
                                               value_cache=values.reshape(batch * 8, 1, 8, 128).to(dev),
                                               accepted_cache_locs=locs.to(dev), accept_lens=lens.to(dev),
                                               accept_offsets=None, state_slots=slots.to(dev))
             torch.cuda.synchronize()
-            torch.testing.assert_close(output.cpu()[slots.long()], exp_out, **TOL)
-            torch.testing.assert_close(lse.cpu()[slots.long()], exp_lse, **TOL)
+            # the reference test's own tolerances against the fp32 restatement ...
+            torch.testing.assert_close(output.cpu()[slots.long()], exp_out, **REF_TOL)
+            torch.testing.assert_close(lse.cpu()[slots.long()], exp_lse, **REF_TOL)
+            # ... and 1e-5 relative against the fp64 evaluation of every merge so far
+            sr.check(output.cpu()[slots.long()], lse.cpu()[slots.long()], x_out, x_lse, x_mag,
+                     what=f"Hq={q_heads} B={batch} step {step}")
         # rows not addressed by a slot are untouched, as is the other half of the view
         untouched = torch.ones(capacity, dtype=torch.bool)
         untouched[slots.long()] = False
@@ -85,11 +96,10 @@ def test_compact_locations_and_offsets(dev):
     torch.cuda.synchronize()
     assert torch.equal(offsets.cpu(), offs.to(torch.int32))
     values = cache[fixed.reshape(-1), 0].reshape(batch, 8, hkv, 128)
-    ref_o, ref_l = osm.merge_accepted_positions(out0, lse0, scores, values, lens)
+    ref_o, ref_l, mag = sr.merged(out0.double(), lse0.double(), out0.double().abs(), query, keys, values, lens, 0.1)
     # accept_len 0 leaves the state row unchanged (documented contract)
-    ref_o[3], ref_l[3] = out0[3], lse0[3]
-    torch.testing.assert_close(out.cpu(), ref_o, **TOL)
-    torch.testing.assert_close(lse.cpu(), ref_l, **TOL)
+    assert torch.equal(out.cpu()[3], out0[3]) and torch.equal(lse.cpu()[3], lse0[3])
+    sr.check(out.cpu(), lse.cpu(), ref_o, ref_l, mag, what="compact locations")
 
 
 @pytest.mark.parametrize("dim,dtype,softcap", [(64, torch.float16, 0.0), (256, torch.bfloat16, 0.0),
@@ -119,13 +129,14 @@ def fused_case(dev, *, layers, batch, hq, hkv, rows, width, capacity, seed, comp
     state = torch.randn(capacity, layers, hq, rows, dim, generator=g)
     lse = torch.randn(capacity, layers, hq, rows, generator=g)
     slots = torch.randperm(capacity, generator=g)[:batch].to(torch.int32)
-    ref_s, ref_l = state.clone(), lse.clone()
+    ref_s, ref_l, ref_m = state.double(), lse.double(), state.double().abs()
     for l in range(layers):
         nk = kc[l][locs.reshape(-1)].reshape(batch, width, hkv, dim)
         nv = vc[l][locs.reshape(-1)].reshape(batch, width, hkv, dim)
-        sc = osm.position_scores(query[l][None].expand(batch, -1, -1, -1), nk, dim ** -.5)
-        o, s = osm.merge_accepted_positions(ref_s[slots.long(), l], ref_l[slots.long(), l], sc, nv, lens)
-        ref_s[slots.long(), l], ref_l[slots.long(), l] = o, s
+        sl = slots.long()
+        o, s, m = sr.merged(ref_s[sl, l], ref_l[sl, l], ref_m[sl, l], query[l][None].expand(batch, -1, -1, -1),
+                            nk, nv, lens, dim ** -.5)
+        ref_s[sl, l], ref_l[sl, l], ref_m[sl, l] = o, s, m
     sd, ld = state.to(dev), lse.to(dev)
     kw = {}
     if compact:
@@ -138,8 +149,7 @@ def fused_case(dev, *, layers, batch, hq, hkv, rows, width, capacity, seed, comp
                            accept_lens=lens.to(dev), state_output=sd, state_lse=ld, softmax_scale=dim ** -.5,
                            state_slots=slots.to(dev), **kw)
     torch.cuda.synchronize()
-    torch.testing.assert_close(sd.cpu(), ref_s, **TOL)
-    torch.testing.assert_close(ld.cpu(), ref_l, **TOL)
+    sr.check(sd.cpu(), ld.cpu(), ref_s, ref_l, ref_m, what=f"fused update L={layers} B={batch} Hq={hq} S={rows}")
 
 
 def test_fused_update_reference_geometry(dev):
@@ -184,5 +194,6 @@ def test_full_prefix_invariant_fp64(dev):
     for b in range(batch):
         n = int(pos[b])
         o_ref, l_ref = osm.full_prefix_state(q[b:b + 1], keys[b:b + 1, :n], vals[b:b + 1, :n], dim ** -.5)
-        assert torch.allclose(out[b].cpu().double(), o_ref[0], rtol=1e-4, atol=1e-5)
-        assert torch.allclose(lse[b].cpu().double(), l_ref[0], rtol=1e-5, atol=1e-5)
+        # magnitude of the summands: the same attention over |v|
+        m_ref, _ = osm.full_prefix_state(q[b:b + 1], keys[b:b + 1, :n], vals[b:b + 1, :n].abs(), dim ** -.5)
+        sr.check(out[b].cpu(), lse[b].cpu(), o_ref[0], l_ref[0], m_ref[0], what=f"full prefix b={b} n={n}")

@@ -325,3 +325,44 @@ def test_assign_fixed_verify_cache_locs_hand_case():
     assert out[2].tolist() == [0, 10, 11, 0, 0, 0, 0, 0]
     assert out[0].tolist() == [0, 0, 0, 0, 0, 0, 20, 21]
     assert int(out[1].abs().sum()) == 0 and int(rtt.abs().sum()) == 0
+
+
+# ---------------------------------------------------------------------------
+# split engine (src/longspark/engine/sampling.py:19-57): hand-worked cases
+# ---------------------------------------------------------------------------
+
+def _split_decision(cand, q, u, p):
+    return ov.decide_acceptance(candidates=cand, sampled_q=q, target_probs=p, uniforms=u)
+
+
+def test_decide_acceptance_hand_cases():
+    from tests import split_cases as sc
+    p, cand, q, u, exp = sc.decide_case()
+    d = _split_decision(cand, q, u, p)
+    assert d.lengths.tolist() == exp["lengths"]
+    assert d.rejected_rows.tolist() == exp["rejected_rows"]
+    assert d.rejection_positions.tolist() == exp["rejection_positions"]
+    for b, j in enumerate(exp["target_row_index"]):
+        assert torch.equal(d.target_rows[b], p[b, j]), b
+
+
+def test_finish_sampling_hand_cases():
+    from tests import split_cases as sc
+    p, cand, q, u, _ = sc.decide_case()
+    d = _split_decision(cand, q, u, p)
+    q_rows, uf, expected = sc.finish_case()
+    assert ov.finish_sampling(d, q_rows, uf).tolist() == expected
+
+
+def test_finish_sampling_mass_threshold_and_clamp():
+    from tests import split_cases as sc
+    cases, (clamp_row, u_clamp, tok_clamp) = sc.threshold_cases()
+    for label, p_row, q_row, uf, tok in cases:
+        p = torch.stack([p_row, p_row])[None]             # [1, gamma + 1 = 2, V]
+        d = _split_decision(torch.tensor([[0]]), torch.tensor([[1.0]]), torch.tensor([[0.5]]), p)
+        assert d.lengths.tolist() == [0] and d.rejected_rows.tolist() == [0], label
+        assert ov.finish_sampling(d, q_row[None], torch.tensor([uf])).tolist() == [tok], label
+    p = torch.stack([torch.tensor([0.0, 1.0, 0.0, 0.0]), clamp_row])[None]
+    d = _split_decision(torch.tensor([[1]]), torch.tensor([[0.5]]), torch.tensor([[0.5]]), p)
+    assert d.lengths.tolist() == [1] and d.rejected_rows.numel() == 0
+    assert ov.finish_sampling(d, torch.zeros(0, 4), torch.tensor([u_clamp])).tolist() == [tok_clamp]
