@@ -229,10 +229,19 @@ __device__ __forceinline__ uint64_t atomic_peek_u64(const uint64_t* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 // Arrive on a counter after this thread's prior atomics completed; returns
-// the previous count.
+// the previous count.  LS_STRICT_ORDER=1 builds the increment as an
+// agent-scope acquire-release RMW instead (ordering in the terms of the HIP
+// memory model, at the cost of an L2 write-back and invalidate per arrival).
+#ifndef LS_STRICT_ORDER
+#define LS_STRICT_ORDER 0
+#endif
 __device__ __forceinline__ uint32_t arrive(uint32_t* counter) {
+#if LS_STRICT_ORDER
+  return __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+#else
   wait_vm();
   return atomic_add_u32(counter, 1u);
+#endif
 }
 
 // Order-preserving map of fp32 to uint32 (larger float -> larger integer;
