@@ -99,6 +99,25 @@ LS_API int ls_verify_greedy(const void* logits, int32_t logits_dtype, int64_t lo
                      uint64_t counter_bytes, void* scratch, uint64_t scratch_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------
+ * ls_verify_greedy without a workspace argument: no counterpart in the
+ * reference.  It is for callers that cannot allocate device memory or pass
+ * a workspace (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid allocation).  The counters live in a 1 MiB device array built
+ * into the library; each GPU the library runs on holds its own copy until
+ * the process ends (its address is looked up, and the array cleared, on the
+ * first call on that device).  Limit: 8*batch*width + 4*batch bytes (each
+ * part rounded up to 256) <= 1 MiB, e.g. batch 4096 x width 16; larger calls
+ * return LS_ERR_WORKSPACE.  All calls on one GPU share the array: calls that
+ * overlap on one GPU (different streams, or different threads' streams)
+ * race and must not be issued.  Arguments and outputs as ls_verify_greedy.
+ * ------------------------------------------------------------------------- */
+LS_API int ls_verify_greedy_noalloc(const void* logits, int32_t logits_dtype, int64_t logits_row_stride,
+                                    const void* candidates, int32_t candidates_dtype, int64_t cand_stride_b,
+                                    int64_t cand_stride_k, int32_t cand_first_col, int64_t batch, int32_t width,
+                                    int64_t vocab, const int32_t* cutoff_verify_lens, int32_t* accept_lens,
+                                    int64_t* bonus, int32_t* truth, int32_t* cap_trim, void* stream);
+
+/* ---------------------------------------------------------------------------
  * Penalty tables from each request's output-token history.
  *
  * Compact form of the accumulated [B, V] penalty tensors the reference keeps

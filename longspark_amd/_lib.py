@@ -148,6 +148,7 @@ _SIGNATURES = {
     "ls_verify_greedy_workspace": (I32, [I64, I32, I64, P, P]),
     "ls_verify_greedy": (I32, [P, I32, I64, P, I32, I64, I64, I32, I64, I32, I64, P, P, P, P, P,
                                P, U64, P, U64, P]),
+    "ls_verify_greedy_noalloc": (I32, [P, I32, I64, P, I32, I64, I64, I32, I64, I32, I64, P, P, P, P, P, P]),
     "ls_penalty_tables": (I32, [P, I64, P, I64, I32, I64, P, P, P, P, I64, P, I64, P, P, P]),
     "ls_adjust_logits": (I32, [P, I32, I64, I64, I64, I32, P, P, I64, P, I64, P, I32, P, I64, I32, I64, P]),
     "ls_add_request_bias": (I32, [P, I32, I64, I64, I64, I32, P, I64, P, I64, I64, P, I64, I32, P]),

@@ -12,6 +12,8 @@
 // vendor/sglang/python/sglang/srt/speculative/dflash_utils.py:564-602.
 #include "common.h"
 
+#include <mutex>
+
 namespace ls {
 namespace {
 
@@ -186,6 +188,47 @@ int launch_greedy(const void* logits, int64_t row_stride, const void* cand, int6
   return LS_OK;
 }
 
+// ------------------------------------------------- allocation-free entry ---
+//
+// ls_verify_greedy_noalloc keeps its counters in this file-scope device
+// array instead of a caller workspace.  Every GPU the library runs on holds
+// its own copy until the process ends.  In host code the array's name is
+// only a host-side stand-in: its device address comes from
+// hipGetSymbolAddress, looked up once per device (with that device current)
+// and kept in noalloc_ptr[], and only that address is passed to kernels.
+constexpr uint64_t kNoAllocBytes = uint64_t(1) << 20;  // 1 MiB: rows*8 + batch*4 (256-byte aligned parts)
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) unsigned char noalloc_scratch[kNoAllocBytes];
+void* noalloc_ptr[kMaxDevices] = {};
+std::mutex noalloc_mutex;
+
+__global__ __launch_bounds__(256) void zero_kernel(uint4* p, uint64_t n16) {
+  for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x; i < n16;
+       i += static_cast<uint64_t>(gridDim.x) * 256)
+    p[i] = make_uint4(0u, 0u, 0u, 0u);
+}
+
+// The current device's copy of the array, set up on the first call on that
+// device: its address from hipGetSymbolAddress, then cleared with a kernel on
+// `stream` (the counters must start at zero; every call leaves them zero).
+int noalloc_counters(hipStream_t stream, void** out) {
+  int dev = 0;
+  LS_CHECK(hipGetDevice(&dev) == hipSuccess, LS_ERR_LAUNCH, "ls_verify_greedy_noalloc: hipGetDevice failed");
+  LS_CHECK(dev >= 0 && dev < kMaxDevices, LS_ERR_VALUE, "ls_verify_greedy_noalloc: device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(noalloc_mutex);
+  if (!noalloc_ptr[dev]) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(noalloc_scratch));
+    LS_CHECK(e == hipSuccess && ptr, LS_ERR_LAUNCH, "ls_verify_greedy_noalloc: hipGetSymbolAddress failed: %s",
+             hipGetErrorString(e));
+    zero_kernel<<<dim3(256), 256, 0, stream>>>(static_cast<uint4*>(ptr), kNoAllocBytes / 16);
+    LS_LAUNCH_CHECK();
+    noalloc_ptr[dev] = ptr;
+  }
+  *out = noalloc_ptr[dev];
+  return LS_OK;
+}
+
 }  // namespace
 }  // namespace ls
 
@@ -239,4 +282,28 @@ extern "C" int ls_verify_greedy(const void* logits, int32_t logits_dtype, int64_
   if (logits_dtype == LS_F32) { LS_GREEDY_CAND(F32) }
 #undef LS_GREEDY_CAND
   return fail(LS_ERR_DTYPE, "ls_verify_greedy: logits must be bf16, fp16 or fp32");
+}
+
+extern "C" int ls_verify_greedy_noalloc(const void* logits, int32_t logits_dtype, int64_t logits_row_stride,
+                                        const void* candidates, int32_t candidates_dtype, int64_t cand_stride_b,
+                                        int64_t cand_stride_k, int32_t cand_first_col, int64_t batch,
+                                        int32_t width, int64_t vocab, const int32_t* cutoff_verify_lens,
+                                        int32_t* accept_lens, int64_t* bonus, int32_t* truth, int32_t* cap_trim,
+                                        void* stream) {
+  using namespace ls;
+  LS_CHECK(batch > 0 && width >= 2 && width <= 64 && vocab > 0, LS_ERR_SHAPE,
+           "ls_verify_greedy_noalloc: need batch > 0, 2 <= width <= 64, vocab > 0 (got %lld, %d, %lld)",
+           (long long)batch, width, (long long)vocab);
+  uint64_t need_c = 0, need_s = 0;
+  ls_verify_greedy_workspace(batch, width, vocab, &need_c, &need_s);
+  LS_CHECK(need_c <= kNoAllocBytes && need_s == 0, LS_ERR_WORKSPACE,
+           "ls_verify_greedy_noalloc: batch %lld x width %d needs %llu bytes of counters; the built-in buffer "
+           "holds %llu (use ls_verify_greedy with a workspace)",
+           (long long)batch, width, (unsigned long long)need_c, (unsigned long long)kNoAllocBytes);
+  void* counters = nullptr;
+  const int rc = noalloc_counters(static_cast<hipStream_t>(stream), &counters);
+  if (rc != LS_OK) return rc;
+  return ls_verify_greedy(logits, logits_dtype, logits_row_stride, candidates, candidates_dtype, cand_stride_b,
+                          cand_stride_k, cand_first_col, batch, width, vocab, cutoff_verify_lens, accept_lens,
+                          bonus, truth, cap_trim, counters, kNoAllocBytes, nullptr, 0, stream);
 }
