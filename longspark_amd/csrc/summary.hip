@@ -78,8 +78,18 @@ __device__ __forceinline__ void stage_rows(const char* kbase, const char* vbase,
   }
 }
 
+// Waves per SIMD the kernel is compiled for.  At head_dim <= 128 the
+// register allocator otherwise puts the MFMA accumulators in AGPRs on top of
+// ~78 VGPRs (4 waves per SIMD, 16 per CU); bounded at 6, the accumulators
+// share the VGPRs (74 in all, no spills) and 24 waves per CU are resident.
+#ifndef LS_SUMMARY_WAVES
+#define LS_SUMMARY_WAVES 6
+#endif
+constexpr int summary_waves(int d) { return d <= 128 ? LS_SUMMARY_WAVES : 2; }
+
 template <int D, int kMode, typename Tag>
-__global__ __launch_bounds__(kSumThreads) void summary_kernel(const ls_summary_args a, int tiles, int wpad) {
+__global__ __launch_bounds__(kSumThreads, summary_waves(D)) void summary_kernel(const ls_summary_args a, int tiles,
+                                                                                int wpad) {
   constexpr bool kScore = kMode != LS_SUMMARY_MERGE;   // computes scores from queries and keys
   constexpr bool kMerge = kMode != LS_SUMMARY_SCORES;  // folds accepted rows into the state
   constexpr int kKB = D / 32;      // 32-deep steps of the score product

@@ -97,7 +97,7 @@ struct Args {
   uint64_t* pubs_t;   // [B*K, S_t, 2]
   uint64_t* pub_d;    // [B, kNBuf]
   uint64_t* pubs_d;   // [B, S_d, 2]
-  struct CandRec* cand_rec;  // [B*K] transformed logit of each row's drafted token
+  int clear_status;    // 1 in the call's first launch: its first workgroup zeroes *status
   int hint;            // which scan kernels the launcher runs (Hint)
   int wave;            // 1: target_wave_kernel runs (takes raw rows with k <= kWaveMaxK)
   int wave_only;       // 1: no workgroup raw scan follows (the wave kernel lists every other raw row)
@@ -1159,13 +1159,10 @@ __device__ __forceinline__ XForm target_xform(const Args& a, int64_t b, int64_t 
 
 // --------------------------------------------------------------- kernels ---
 
-// One thread per target row: the drafted token checked at this row and its
-// logit after penalties and mask (the rows' scans need it only at the end).
+// The drafted token a target row checks and its logit after penalties and
+// mask (tok < 0: none), for the workgroup scans and the exact fallback.
 template <typename TagT, typename CandT>
-__global__ __launch_bounds__(kT) void cand_prep_kernel(Args a) {
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * kT + threadIdx.x;
-  if (row == 0 && a.status) *a.status = 0;  // the first launch of the call clears the status word
-  if (row >= a.batch * a.width) return;
+__device__ __forceinline__ CandRec cand_rec_of(const Args& a, int64_t row) {
   const int64_t b = row / a.width;
   const int j = static_cast<int>(row % a.width);
   CandRec cr{NAN, -1};
@@ -1178,7 +1175,18 @@ __global__ __launch_bounds__(kT) void cand_prep_kernel(Args a) {
       cr.x = transform1(target_xform(a, b, row), to_f32<S>(rp[c]), c);
     }
   }
-  a.cand_rec[row] = cr;
+  return cr;
+}
+
+// The drafted token a target row checks (-1: none), for the wavefront path,
+// which takes its probability from the row's support by index.
+template <typename CandT>
+__device__ __forceinline__ int cand_tok_of(const Args& a, int64_t row) {
+  const int64_t b = row / a.width;
+  const int j = static_cast<int>(row % a.width);
+  if (!a.cand || j >= a.width - 1) return -1;
+  const int64_t c = cand_at<CandT>(a, b, j);
+  return (c >= 0 && c < a.vocab) ? static_cast<int>(c) : -1;
 }
 
 // ------------------------------------------- one wavefront per target row ---
@@ -1589,9 +1597,13 @@ __device__ __forceinline__ void wave_scan_candidates(WaveShared& ws, const typen
 // the row record and support.  A row the candidates cannot resolve (ovf) is
 // listed for the exact fallback with its raw maximum.  Returns the record
 // (the same in every lane).
+// With cand_by_match the drafted token's probability is that of its support
+// entry, found by index (0 when it is not in the support): the support holds
+// exactly the keys at or above the record's last key, so this is the value
+// the cand_x form gives, without reading the token's logit.
 __device__ RowRec wave_finalize_topk(WaveShared& ws, int count, const Params& p, float raw_max, int ovf, RowRec* rec,
                                    int32_t* sidx, float* sp, int cand_tok, float cand_x, uint32_t* list_cnt,
-                                   int32_t* list, int32_t list_id) {
+                                   int32_t* list, int32_t list_id, bool cand_by_match = false) {
   const int lane = threadIdx.x & (kWave - 1);
   const int k = p.top_k;
   const float t = p.temperature;
@@ -1648,7 +1660,11 @@ __device__ RowRec wave_finalize_topk(WaveShared& ws, int count, const Params& p,
     const uint64_t lastk = __shfl(key, n_f > 0 ? n_f - 1 : 0, kWave);
     rr.last = n_f > 0 ? lastk : ~uint64_t(0);
     rr.p_cand = 0.f;
-    if (cand_tok >= 0) {
+    if (cand_tok >= 0 && cand_by_match) {
+      const uint64_t hit = __ballot(lane < n_f && key_idx(key) == cand_tok);
+      const float pv = __shfl(e / zf, hit ? __ffsll(static_cast<long long>(hit)) - 1 : 0, kWave);
+      rr.p_cand = hit ? pv : 0.f;
+    } else if (cand_tok >= 0) {
       const float sc = cand_x / t;
       const uint64_t kc = cand_key(sc, cand_tok);
       rr.p_cand = (kc >= rr.last && rr.n != 0) ? __expf(sc - rr.m) / rr.z : 0.f;
@@ -1749,7 +1765,14 @@ __device__ RowRec wave_finalize_topk(WaveShared& ws, int count, const Params& p,
   rr.why = 0;
   rr.last = n_f > 0 ? ws.buf[n_f - 1] : ~uint64_t(0);
   rr.p_cand = 0.f;
-  if (cand_tok >= 0) {
+  if (cand_tok >= 0 && cand_by_match) {
+    float pv = 0.f;
+    for (int i = lane; i < n_f; i += kWave) {
+      const uint64_t kk = ws.buf[i];
+      if (key_idx(kk) == cand_tok) pv = __expf(key_s(kk) - m) / zf;
+    }
+    rr.p_cand = wave_max(pv);  // at most one entry matches; probabilities are >= 0
+  } else if (cand_tok >= 0) {
     const float sc = cand_x / t;
     const uint64_t kc = cand_key(sc, cand_tok);
     rr.p_cand = (kc >= rr.last && rr.n != 0) ? __expf(sc - rr.m) / rr.z : 0.f;
@@ -1770,9 +1793,8 @@ __global__ __launch_bounds__(kT) void target_scan_kernel(Args a) {
   using S = typename TagT::storage;
   const S* rp = static_cast<const S*>(a.logits) + row * a.lrs;
   const XForm f = target_xform(a, b, row);
-  // Drafted token and its transformed logit, prepared by cand_prep_kernel
-  // (a dependent chain of loads kept off the scan's critical path).
-  const CandRec cr = a.cand_rec[row];
+  if (a.clear_status && blockIdx.x == 0 && threadIdx.x == 0 && a.status) *a.status = 0;
+  const CandRec cr = cand_rec_of<TagT, CandT>(a, row);
   process_row<TagT, kVec, kPath>(sh, rp, a.vocab, p, f, a.s_t, slice, a.pub_t + row * kNBuf,
                                  a.pubs_t + row * a.s_t * 2, a.cnt_t + row, a.rec_t + row,
                                  a.sidx_t + row * kCap, a.sp_t + row * kCap, cr.tok, cr.x, a.list_cnt,
@@ -2131,6 +2153,7 @@ __global__ __launch_bounds__(kWave, 2) void verify_wave_kernel(Args a) {
   using S = typename TagT::storage;
   constexpr int P = TagT::kPerVec;
   const int64_t rows = a.batch * a.width;
+  if (a.clear_status && blockIdx.x == 0 && threadIdx.x == 0 && a.status) *a.status = 0;
   if (static_cast<int64_t>(blockIdx.x) >= rows) {
     const int64_t d = blockIdx.x - rows;
     draft_wave_slice<TagD, CandT, true>(a, ws, d / a.dslices, static_cast<int>(d % a.dslices));
@@ -2170,14 +2193,14 @@ __global__ __launch_bounds__(kWave, 2) void verify_wave_kernel(Args a) {
       a.list_t[atomic_add_u32(a.list_cnt, 1u)] = static_cast<int32_t>(row);
     }
   } else {
-    const CandRec cr = a.cand_rec[row];
+    const int cand_tok = cand_tok_of<CandT>(a, row);
     int count, ovf;
     float raw_max;
     float kth;
     wave_scan_candidates<TagT>(ws, rp, a.vocab, 0, f, p.top_k, r, q, count, raw_max, kth, ovf);
     const RowRec rr = wave_finalize_topk(ws, count, p, raw_max, ovf, a.rec_t + row, a.sidx_t + row * kCap,
-                                         a.sp_t + row * kCap, cr.tok, cr.x, a.list_cnt, a.list_t,
-                                         static_cast<int32_t>(row));
+                                         a.sp_t + row * kCap, cand_tok, NAN, a.list_cnt, a.list_t,
+                                         static_cast<int32_t>(row), true);
     word = (static_cast<uint64_t>(static_cast<uint32_t>(rr.flags)) << 32) | __float_as_uint(rr.p_cand);
   }
   if (a.fuse_draft && lane == 0) atomic_put_u64(a.acc_t + row, word | kAccPublished);
@@ -2215,7 +2238,7 @@ __device__ __noinline__ void write_exact_record(Shared& sh, const Exact& ex, int
 
 // Exact support of one target row the scans could not resolve; rewrites its
 // record and support.  Called by the whole workgroup.
-template <typename TagT>
+template <typename TagT, typename CandT>
 __device__ __forceinline__ void target_exact_row(Shared& sh, const Args& a, int64_t row) {
   const int64_t b = row / a.width;
   const RowRec prev = a.rec_t[row];
@@ -2224,7 +2247,7 @@ __device__ __forceinline__ void target_exact_row(Shared& sh, const Args& a, int6
   using S = typename TagT::storage;
   const S* rp = static_cast<const S*>(a.logits) + row * a.lrs;
   const XForm f = target_xform(a, b, row);
-  const CandRec cr = a.cand_rec[row];
+  const CandRec cr = cand_rec_of<TagT, CandT>(a, row);
   const int mode = row_mode(p, a.vocab);
   float m_x = prev.m;
   double z = prev.z;
@@ -2239,7 +2262,7 @@ template <typename TagT, typename CandT>
 __global__ __launch_bounds__(kT) void target_fallback_kernel(Args a) {
   __shared__ Shared sh;
   const uint32_t n = *a.list_cnt;
-  for (uint32_t li = blockIdx.x; li < n; li += gridDim.x) target_exact_row<TagT>(sh, a, a.list_t[li]);
+  for (uint32_t li = blockIdx.x; li < n; li += gridDim.x) target_exact_row<TagT, CandT>(sh, a, a.list_t[li]);
 }
 
 // Exact support of request b's draft row at position len (a row the draft
@@ -2638,7 +2661,7 @@ __global__ __launch_bounds__(kT) void resolve_kernel(Args a) {
     const int64_t trow = b * a.width + s_len;
     if (trow == tried) break;  // still unresolved (capacity): the request is blocked
     tried = trow;
-    target_exact_row<TagT>(sh, a, trow);
+    target_exact_row<TagT, CandT>(sh, a, trow);
     __syncthreads();
   }
   RowRec dm{};  // the merged draft record (wave 0)
@@ -2754,7 +2777,7 @@ int pick_slices(int64_t rows, int64_t vocab, int want_wgs, int max_top_k) {
 struct Layout {
   uint64_t counters, scratch;
   uint64_t off_rec_t, off_sidx_t, off_sp_t, off_rec_d, off_sidx_d, off_sp_d, off_pub_t, off_pubs_t, off_pub_d,
-      off_pubs_d, off_list_t, off_list_d, off_cand;
+      off_pubs_d, off_list_t, off_list_d;
   int s_t, s_d;
 };
 
@@ -2777,7 +2800,6 @@ Layout layout(int64_t batch, int width, int64_t vocab, int max_top_k) {
   l.off_pubs_d = o; o += up256(16ull * batch * (l.s_d > kDraftSlices ? l.s_d : kDraftSlices));
   l.off_list_t = o; o += up256(4ull * rows);
   l.off_list_d = o; o += up256(4ull * batch);
-  l.off_cand = o; o += up256(sizeof(CandRec) * rows);
   l.scratch = o;
   return l;
 }
@@ -2859,7 +2881,6 @@ extern "C" int ls_verify_sample(const ls_verify_sample_args* in, void* counters,
   a.pubs_d = reinterpret_cast<uint64_t*>(s + l.off_pubs_d);
   a.list_t = reinterpret_cast<int32_t*>(s + l.off_list_t);
   a.list_d = reinterpret_cast<int32_t*>(s + l.off_list_d);
-  a.cand_rec = reinterpret_cast<CandRec*>(s + l.off_cand);
   a.s_t = l.s_t;
   a.s_d = l.s_d;
   a.hint = x.scan_hint;
@@ -2867,8 +2888,7 @@ extern "C" int ls_verify_sample(const ls_verify_sample_args* in, void* counters,
   hipStream_t st = static_cast<hipStream_t>(stream);
 
   const dim3 g_t(static_cast<unsigned>(rows * l.s_t)), g_d(static_cast<unsigned>(x.batch * l.s_d)),
-      g_r(static_cast<unsigned>(x.batch)), g_f(static_cast<unsigned>(rows < 256 ? rows : 256)),
-      g_c(static_cast<unsigned>((rows + rs::kT - 1) / rs::kT));
+      g_r(static_cast<unsigned>(x.batch)), g_f(static_cast<unsigned>(rows < 256 ? rows : 256));
   void* const* ev = x.timing_events;
 #define LS_EVENT(i)                                                                              \
   do {                                                                                           \
@@ -2883,8 +2903,7 @@ extern "C" int ls_verify_sample(const ls_verify_sample_args* in, void* counters,
     using DS = typename TD::storage;                                                                          \
     const bool tv = tvec_ok && (x.logits_row_stride * sizeof(TS)) % 16 == 0;                                  \
     const bool dv = dvec_ok && (x.draft_stride_b * sizeof(DS)) % 16 == 0 && (x.draft_stride_k * sizeof(DS)) % 16 == 0; \
-    cand_prep_kernel<TT, CT><<<g_c, rs::kT, 0, st>>>(a);                                                      \
-    LS_LAUNCH_CHECK();                                                                                        \
+    a.clear_status = 1; /* the first launch below zeroes the status word */                                   \
     a.wave = (a.hint != kHintExactOnly && tv && x.vocab / TT::kPerVec >= int64_t(kWave) * kWaveDepth) ? 1 : 0; \
     a.wave_only = (a.wave && x.max_top_k > 0 && x.max_top_k <= kWaveMaxRowK) ? 1 : 0;                          \
     a.dslices = static_cast<int>(x.vocab / (TD::kPerVec * kWave * kWaveDepth) < kDraftSlicesUsed              \
@@ -2898,17 +2917,17 @@ extern "C" int ls_verify_sample(const ls_verify_sample_args* in, void* counters,
     if (a.wave) {                                                                                             \
       const int64_t nwg = rows + (a.fuse_draft ? x.batch * a.dslices : 0);                                    \
       verify_wave_kernel<TT, TD, CT><<<dim3(static_cast<unsigned>(nwg)), kWave, 0, st>>>(a);                 \
-      LS_LAUNCH_CHECK();                                                                                      \
+      LS_LAUNCH_CHECK(); a.clear_status = 0;                                                                  \
     }                                                                                                         \
     if (a.hint != kHintExactOnly && !a.wave_only) {                                                           \
       if (tv) target_scan_kernel<TT, true, CT, kPathRaw><<<g_t, rs::kT, 0, st>>>(a);                         \
       else target_scan_kernel<TT, false, CT, kPathRaw><<<g_t, rs::kT, 0, st>>>(a);                           \
-      LS_LAUNCH_CHECK();                                                                                      \
+      LS_LAUNCH_CHECK(); a.clear_status = 0;                                                                  \
     }                                                                                                         \
     if (a.hint != kHintRawOnly) {                                                                             \
       if (tv) target_scan_kernel<TT, true, CT, kPathExact><<<g_t, rs::kT, 0, st>>>(a);                       \
       else target_scan_kernel<TT, false, CT, kPathExact><<<g_t, rs::kT, 0, st>>>(a);                         \
-      LS_LAUNCH_CHECK();                                                                                      \
+      LS_LAUNCH_CHECK(); a.clear_status = 0;                                                                  \
     }                                                                                                         \
     if (ev) LS_EVENT(1);                                                                                      \
     if (!a.inline_fb) {                                                                                       \
@@ -3008,35 +3027,32 @@ extern "C" int ls_target_probs(const ls_target_probs_args* in, void* counters, u
   a.pubs_d = reinterpret_cast<uint64_t*>(s + l.off_pubs_d);
   a.list_t = reinterpret_cast<int32_t*>(s + l.off_list_t);
   a.list_d = reinterpret_cast<int32_t*>(s + l.off_list_d);
-  a.cand_rec = reinterpret_cast<CandRec*>(s + l.off_cand);
   a.s_t = l.s_t;
   a.s_d = l.s_d;
   a.hint = x.scan_hint;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const dim3 g_t(static_cast<unsigned>(rows * l.s_t)), g_f(static_cast<unsigned>(rows < 256 ? rows : 256)),
-      g_c(static_cast<unsigned>((rows + rs::kT - 1) / rs::kT)), g_r(static_cast<unsigned>(rows));
+  const dim3 g_t(static_cast<unsigned>(rows * l.s_t)), g_f(static_cast<unsigned>(rows < 256 ? rows : 256)), g_r(static_cast<unsigned>(rows));
   const bool tvec_ok = aligned16(x.logits);
 #define LS_TP(TT)                                                                                             \
   do {                                                                                                        \
     using TS = typename TT::storage;                                                                          \
     const bool tv = tvec_ok && (x.logits_row_stride * sizeof(TS)) % 16 == 0;                                  \
-    cand_prep_kernel<TT, int32_t><<<g_c, rs::kT, 0, st>>>(a);                                                 \
-    LS_LAUNCH_CHECK();                                                                                        \
+    a.clear_status = 1; /* the first launch below zeroes the status word */                                   \
     a.wave = (a.hint != kHintExactOnly && tv && x.vocab / TT::kPerVec >= int64_t(kWave) * kWaveDepth) ? 1 : 0; \
     a.wave_only = (a.wave && x.max_top_k > 0 && x.max_top_k <= kWaveMaxRowK) ? 1 : 0;                          \
     if (a.wave) {                                                                                             \
       verify_wave_kernel<TT, F32, int32_t><<<dim3(static_cast<unsigned>(rows)), kWave, 0, st>>>(a);          \
-      LS_LAUNCH_CHECK();                                                                                      \
+      LS_LAUNCH_CHECK(); a.clear_status = 0;                                                                  \
     }                                                                                                         \
     if (a.hint != kHintExactOnly && !a.wave_only) {                                                           \
       if (tv) target_scan_kernel<TT, true, int32_t, kPathRaw><<<g_t, rs::kT, 0, st>>>(a);                    \
       else target_scan_kernel<TT, false, int32_t, kPathRaw><<<g_t, rs::kT, 0, st>>>(a);                      \
-      LS_LAUNCH_CHECK();                                                                                      \
+      LS_LAUNCH_CHECK(); a.clear_status = 0;                                                                  \
     }                                                                                                         \
     if (a.hint != kHintRawOnly) {                                                                             \
       if (tv) target_scan_kernel<TT, true, int32_t, kPathExact><<<g_t, rs::kT, 0, st>>>(a);                  \
       else target_scan_kernel<TT, false, int32_t, kPathExact><<<g_t, rs::kT, 0, st>>>(a);                    \
-      LS_LAUNCH_CHECK();                                                                                      \
+      LS_LAUNCH_CHECK(); a.clear_status = 0;                                                                  \
     }                                                                                                         \
     target_fallback_kernel<TT, int32_t><<<g_f, rs::kT, 0, st>>>(a);                                           \
     LS_LAUNCH_CHECK();                                                                                        \
