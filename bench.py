@@ -39,9 +39,9 @@ V = 151936
 TRAFFIC = {
     "verify_wave_kernel": (712_314_120, "profiles/verify_wave_kernel_verify_sample_B128_K16_V151936.md"),
     "greedy_verify_kernel": (622_640_864, "profiles/greedy_verify_kernel_B128_K16_V151936.md"),
-    "window_gather_kernel": (604_246_324, "profiles/window_gather_kernel_B8_L36_Hkv8_D128_ctx131072.md"),
+    "window_gather_kernel": (604_552_647, "profiles/window_gather_kernel_B8_L36_Hkv8_D128_ctx131072.md"),
     "summary_kernel": (646_838_203, "profiles/summary_kernel_B8_L36_R256_W16.md"),
-    "softmax_temp_kernel": (2_383_427_050, "profiles/softmax_temp_kernel_B128_K16_V151936.md"),
+    "softmax_temp_resident_kernel": (1_868_715_744, "profiles/softmax_temp_resident_kernel_B128_K16_V151936.md"),
     "chain_kernel": (158_497_097, "profiles/chain_kernel_chain_sampling_B128_K16_V151936.md"),
     "request_bias_kernel": (1_403_662_037, "profiles/request_bias_kernel_adjust_logits_B128_K16_V151936.md"),
     "sample_step_kernel": (156_653_721, "profiles/sample_step_kernel_B128_V151936.md"),
@@ -421,7 +421,7 @@ class SoftmaxTempWorkload:
         rows = batch * width
         self.bytes = rows * vocab * 2 + rows * vocab * 4   # read the logits once, write the probabilities once
         self.units = self.bytes / 1e9
-        self.kernel = "softmax_temp_kernel"
+        self.kernel = "softmax_temp_resident_kernel"
 
     def step(self):
         from longspark_amd import dense
@@ -514,6 +514,36 @@ class HbmCopy:
         med, n = time_cpu(lambda: b.copy_(a))
         return {"value": 2 * a.numel() * 2 / med / 1e9, "threads": threads,
                 "sample": f"128 MiB host copy, median of {n} runs"}
+
+
+class HbmFill:
+    """Device fill of 1 GiB (torch fill_): the write-only rate, beside the
+    copy's mixed read/write rate, for kernels whose traffic is mostly writes
+    (SoftmaxTemp writes 2 bytes of fp32 output for every byte of bf16 it reads)."""
+
+    name = "hbm_fill"
+    metric = "device fill GB/s (write) of 1 GiB"
+    unit = "GB/s"
+
+    def __init__(self, dev, nbytes=1 << 30):
+        self.dst = torch.empty(nbytes // 4, dtype=torch.float32, device=dev)
+        self.bytes = nbytes
+        self.units = self.bytes / 1e9
+        self.kernel = "fill"
+        self.dtype = "f32"
+
+    def step(self):
+        self.dst.fill_(1.0)
+
+    def config(self):
+        return {"workload": "torch fill_ of 1 GiB fp32 (write-only rate)", "bytes": self.bytes}
+
+    def cpu_baseline(self, threads):
+        torch.set_num_threads(threads)
+        a = torch.empty(1 << 25, dtype=torch.float32)
+        med, n = time_cpu(lambda: a.fill_(1.0))
+        return {"value": a.numel() * 4 / med / 1e9, "threads": threads,
+                "sample": f"128 MiB host fill, median of {n} runs"}
 
 
 class ChainSampling:
@@ -949,7 +979,7 @@ class AdjustLogits:
 
 WORKLOADS = {w.name: w for w in (GreedyVerify, StochasticVerify, StochasticVerifyHighAccept, WindowGather, SummaryUpdate, SoftmaxTempWorkload,
                                   TargetProbsWorkload, ChainSampling, AdjustLogits, SampleStep, Global16Prefill, DraftAttention,
-                                  DraftMerge, FullRound, HbmCopy)}
+                                  DraftMerge, FullRound, HbmCopy, HbmFill)}
 DEFAULT_WORKLOAD = "verify_sample"
 
 

@@ -23,7 +23,7 @@ namespace ls {
 namespace {
 
 constexpr int kGT = 256;       // threads per workgroup
-constexpr int kChunk = 16;     // window tokens per workgroup
+constexpr int kChunk = 8;      // window tokens per workgroup
 
 template <typename T>
 __device__ __forceinline__ int64_t ld_index(const void* p, int64_t i) {
@@ -96,10 +96,15 @@ __device__ __forceinline__ uint4 load16_global_stream(const char* p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
-// One workgroup: kChunk window tokens of one (request, layer, K or V).
-// The chunk's physical rows are resolved once into LDS, then every thread
-// copies 16-byte vectors: (head h, window token i, vector c) with c fastest,
-// then i, so a wave writes contiguous runs of one head's output rows.
+// One workgroup: kChunk window tokens of one (request, layer), keys and
+// values.  The chunk's physical rows are resolved once into LDS (for both),
+// then every thread copies 16-byte vectors: (K or V, head h, window token i,
+// vector c) with c fastest, then i, so a wave writes contiguous runs of one
+// head's output rows.  Each thread issues its kU loads, then its kU stores,
+// and the workgroup ends: a second round of loads in the same thread would
+// wait for the first round's stores (one counter covers both), so more,
+// shorter workgroups stream faster (8 tokens x K and V: 2,048 vectors per
+// workgroup, 61 registers, 8 waves per SIMD).
 // kVph = 16-byte vectors per head row when it is a power of two the kernel
 // was built for (index math by shifts), 0 = any (runtime division).
 template <int kVph>
@@ -109,8 +114,6 @@ __global__ __launch_bounds__(kGT) void window_gather_kernel(GatherArgs a) {
   int64_t w = blockIdx.x;
   const int chunk = static_cast<int>(w % chunks);
   w /= chunks;
-  const int kv = static_cast<int>(w % 2);
-  w /= 2;
   const int layer = static_cast<int>(w % a.n_layers);
   const int64_t b = w / a.n_layers;
   const int64_t seq = ld_any(a.seq_lens, a.seq_dtype, b);
@@ -128,12 +131,14 @@ __global__ __launch_bounds__(kGT) void window_gather_kernel(GatherArgs a) {
     locs[threadIdx.x] = loc;
   }
   __syncthreads();
-  const char* src = reinterpret_cast<const char*>((kv ? a.v_layers : a.k_layers)[layer]);
-  char* dst = a.out + (b * a.osb + layer * a.osl + kv * a.oskv) * a.esize;
+  const char* srck = reinterpret_cast<const char*>(a.k_layers[layer]);
+  const char* srcv = reinterpret_cast<const char*>(a.v_layers[layer]);
+  char* dst = a.out + (b * a.osb + layer * a.osl) * a.esize;
   const int vph = kVph ? kVph : a.head_dim * a.esize / 16;
   const int ntok = min(kChunk, a.window - i0);
   const int per_head = kChunk * vph;   // tokens past ntok are skipped
-  const int total = a.heads * per_head;
+  const int per_kv = a.heads * per_head;
+  const int total = 2 * per_kv;
   constexpr int kU = 8;
   for (int j0 = threadIdx.x; j0 < total; j0 += kGT * kU) {
     uint4 v[kU];
@@ -141,16 +146,18 @@ __global__ __launch_bounds__(kGT) void window_gather_kernel(GatherArgs a) {
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
       const int j = j0 + u * kGT;
-      const int h = j / per_head;
-      const int r = j - h * per_head;
+      const int kv = j >= per_kv;
+      const int jh = j - kv * per_kv;
+      const int h = jh / per_head;
+      const int r = jh - h * per_head;
       const int ti = r / vph;
       const int c = r - ti * vph;
       const bool live = j < total && ti < ntok;
       const int64_t loc = live ? locs[ti] : -1;
-      dp[u] = live ? dst + (h * a.osh + static_cast<int64_t>(i0 + ti) * a.osw) * a.esize + c * 16 : nullptr;
+      dp[u] = live ? dst + (kv * a.oskv + h * a.osh + static_cast<int64_t>(i0 + ti) * a.osw) * a.esize + c * 16 : nullptr;
       // rows past raw and dead lanes read head 0 of row 0 (in bounds); rows
       // past raw store zeros, dead lanes store nothing
-      v[u] = load16_global_stream(src + ((loc < 0 ? 0 : loc) * a.token_stride + (live ? h : 0) * a.head_stride) *
+      v[u] = load16_global_stream((kv ? srcv : srck) + ((loc < 0 ? 0 : loc) * a.token_stride + (live ? h : 0) * a.head_stride) *
                                             a.esize + c * 16);
       if (loc < 0) v[u] = make_uint4(0, 0, 0, 0);
     }
@@ -158,7 +165,7 @@ __global__ __launch_bounds__(kGT) void window_gather_kernel(GatherArgs a) {
     for (int u = 0; u < kU; ++u)
       if (dp[u]) store16_stream(dp[u], v[u]);
   }
-  if (a.raw_out && threadIdx.x == 0 && layer == 0 && kv == 0 && chunk == 0) a.raw_out[b] = static_cast<int32_t>(raw);
+  if (a.raw_out && threadIdx.x == 0 && layer == 0 && chunk == 0) a.raw_out[b] = static_cast<int32_t>(raw);
 }
 
 struct AppendArgs {
@@ -277,7 +284,7 @@ extern "C" int ls_kv_window_gather(const uint64_t* k_layers, const uint64_t* v_l
   a.osb = out_stride_b; a.osl = out_stride_l; a.oskv = out_stride_kv; a.osh = out_stride_h; a.osw = out_stride_w;
   a.raw_out = raw_lengths;
   const int64_t chunks = (window + kChunk - 1) / kChunk;
-  const int64_t grid = batch * n_layers * 2 * chunks;
+  const int64_t grid = batch * n_layers * chunks;
   LS_CHECK(grid < (int64_t(1) << 31), LS_ERR_SHAPE, "ls_kv_window_gather: grid too large");
   const dim3 g(static_cast<unsigned>(grid));
   hipStream_t st = static_cast<hipStream_t>(stream);

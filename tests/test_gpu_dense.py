@@ -100,6 +100,26 @@ def test_softmax_temp_fp16_strided(dev):
     check_softmax(got, logits, temps, 4, "fp16 strided")
 
 
+def test_softmax_temp_bf16_resident_tail_and_masked(dev):
+    """A 16-bit row held in registers with 3 trailing entries past its last
+    4-entry unit, masked entries, a row that is masked but for its last 4
+    entries, and a row stride wider than the vocabulary (16-byte aligned)."""
+    g = torch.Generator().manual_seed(54)
+    wide = (3.0 * torch.randn(6, 30008, generator=g)).to(torch.bfloat16)
+    logits = wide[:, :30003].clone()
+    logits[1, ::5] = float("-inf")
+    logits[3, :29999] = float("-inf")
+    temps = torch.tensor([0.9, 1.4, 0.5])
+    print("softmax_temp bf16 6 x 30003 (row stride 30008)", flush=True)
+    wide_d = wide.to(dev)
+    wide_d[:, :30003] = logits.to(dev)
+    got = dense.softmax_temp(logits=wide_d[:, :30003], temperatures=temps.to(dev), rows_per_request=2)
+    torch.cuda.synchronize()
+    masked = torch.isneginf(logits.float())
+    assert bool((got.cpu()[masked] == 0).all()), "masked entries must be exactly 0"
+    check_softmax(got, logits, temps, 2, "bf16 resident tail")
+
+
 def run_target_probs(dev, logits, params, rows_per_request, max_top_k=None, min_p=False):
     got = dense.target_probs(logits=logits.to(dev), temperatures=params.temperatures.to(dev),
                              rows_per_request=rows_per_request, top_ks=params.top_ks.to(dev),
