@@ -44,7 +44,9 @@ constexpr float kLn2 = 0.6931471805599453f;
 template <int D>
 struct PrefillShape {
   static constexpr int kBlk = D == 64 ? 64 : 32;    // prefix tokens per step
-  static constexpr int kKP = D + 8;                   // 16-bit elements per LDS key row
+  static constexpr int kKP = D + 16;                  // 16-bit elements per LDS key / query row: a 32-byte skew per
+                                                      // row keeps a 16-lane x 16-byte row read on distinct banks of
+                                                      // gfx950's 64-bank LDS (D + 8 stalled 25% of LDS cycles)
   static constexpr int kVP = kBlk + 4;                // 16-bit elements per LDS transposed value row
   static constexpr int kChunks = D / 8;               // 16-byte vectors per row
   static constexpr int kKVecs = kBlk * kChunks;       // key vectors per step

@@ -94,7 +94,7 @@ __global__ __launch_bounds__(kSumThreads, summary_waves(D)) void summary_kernel(
   constexpr bool kMerge = kMode != LS_SUMMARY_SCORES;  // folds accepted rows into the state
   constexpr int kKB = D / 32;      // 32-deep steps of the score product
   constexpr int kDB = D / 16;      // 16-column blocks of the state
-  constexpr int kKPitch = D + 8;   // 16-bit elements per LDS key row
+  constexpr int kKPitch = D + 16;  // 16-bit elements per LDS key row (32-byte skew: distinct banks of the 64-bank LDS)
   constexpr int kVPitch = D + 4;   // fp32 per LDS value row: rows 4 apart land 16 banks apart
   extern __shared__ __align__(16) char smem[];
   __shared__ int64_t s_koff[kMaxWidth], s_voff[kMaxWidth];
@@ -323,7 +323,7 @@ int summary_entry(const ls_summary_args* ap, void* stream, const char* what) {
   const int64_t grid = a.batch * a.layers * a.kv_heads * tiles;
   LS_CHECK(grid < (int64_t(1) << 31), LS_ERR_SHAPE, "%s: grid too large", what);
   const int d = a.head_dim;
-  const size_t lds = (kScore ? static_cast<size_t>(wpad) * (d + 8) * 2 : 0) +
+  const size_t lds = (kScore ? static_cast<size_t>(wpad) * (d + 16) * 2 : 0) +
                      (kMerge ? static_cast<size_t>(wpad) * (d + 4) * 4 : 0);
   hipStream_t st = static_cast<hipStream_t>(stream);
   switch (d) {
