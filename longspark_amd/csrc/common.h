@@ -153,6 +153,32 @@ __device__ __forceinline__ int wave_sum_i(int v) {
   return v;
 }
 
+// Reductions over the 4 lanes i, i ^ 16, i ^ 32, i ^ 48 (one column of a
+// 16x16 MFMA result, held 4 rows per lane) with gfx950's VALU lane swaps
+// instead of LDS permutes: v_permlane16_swap leaves every lane with the
+// value of its row pair's even row and of its odd row, v_permlane32_swap
+// with the value of its lower-half and its upper-half lane.  The sums pair
+// the same operands as the xor-16 then xor-32 butterfly, so they are
+// bit-identical to it.
+__device__ __forceinline__ float row_pair16_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float row_pair32_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float row_pair16_max(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float row_pair32_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float col4_sum(float v) { return row_pair32_sum(row_pair16_sum(v)); }
+__device__ __forceinline__ float col4_max(float v) { return row_pair32_max(row_pair16_max(v)); }
+
 // (value, index) argmax with torch semantics: larger value wins, equal values
 // keep the lower index.
 struct ArgMax {

@@ -79,8 +79,7 @@ __device__ __forceinline__ void fold(RowState& st, f32x4_t (&sc)[kTiles], VT vt)
   for (int t = 0; t < kTiles; ++t)
 #pragma unroll
     for (int i = 0; i < 4; ++i) bm = fmaxf(bm, sc[t][i]);
-  bm = fmaxf(bm, __shfl_xor(bm, 16, kWave));
-  bm = fmaxf(bm, __shfl_xor(bm, 32, kWave));
+  bm = col4_max(bm);
   const float mn = fmaxf(st.m, bm);
   // a row with nothing visible yet keeps m = -inf: subtract 0 instead
   const float base = mn == -__builtin_inff() ? 0.f : mn;
@@ -263,8 +262,7 @@ __global__ __launch_bounds__(1024) void draft_attention_kernel(const ls_draft_at
   }
 
   float z = st.z;
-  z += __shfl_xor(z, 16, kWave);
-  z += __shfl_xor(z, 32, kWave);
+  z = col4_sum(z);
   if (!row_ok) return;
   const float inv = 1.f / z;
   uint16_t* out = static_cast<uint16_t*>(a.output) + b * a.o_stride_b + head * a.o_stride_h + c16 * a.o_stride_r;
@@ -283,14 +281,8 @@ __global__ __launch_bounds__(1024) void draft_attention_kernel(const ls_draft_at
 // sources are normalised on their own and the three merged by their LSEs.
 // One wave per query head; no LDS.
 
-__device__ __forceinline__ float row_max4(float v) {
-  v = fmaxf(v, __shfl_xor(v, 16, kWave));
-  return fmaxf(v, __shfl_xor(v, 32, kWave));
-}
-__device__ __forceinline__ float row_sum4(float v) {
-  v += __shfl_xor(v, 16, kWave);
-  return v + __shfl_xor(v, 32, kWave);
-}
+__device__ __forceinline__ float row_max4(float v) { return col4_max(v); }
+__device__ __forceinline__ float row_sum4(float v) { return col4_sum(v); }
 
 // kMaxThreads bounds the workgroup (64 x query heads per KV head); the
 // smaller bounds leave the compiler registers for the loads issued up front.

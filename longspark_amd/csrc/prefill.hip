@@ -273,8 +273,7 @@ __device__ __forceinline__ void prefill_body(const ls_prefill_args& a, const Pre
     for (int nt = 0; nt < Sh::kNT; ++nt)
 #pragma unroll
       for (int i = 0; i < 4; ++i) bm = fmaxf(bm, sc[nt][i]);
-    bm = fmaxf(bm, __shfl_xor(bm, 16, kWave));
-    bm = fmaxf(bm, __shfl_xor(bm, 32, kWave));
+    bm = col4_max(bm);
     // finite after the first step (it holds at least one prefix token); a
     // padding step past the prefix leaves m unchanged and adds nothing
     const float mn = fmaxf(m, bm);
@@ -351,8 +350,7 @@ __device__ __forceinline__ void prefill_body(const ls_prefill_args& a, const Pre
     if (wave_rows) compute(tb + kBlk);
   }
   if (!valid) return;
-  z += __shfl_xor(z, 16, kWave);
-  z += __shfl_xor(z, 32, kWave);
+  z = col4_sum(z);
 
   if (direct) {
     const float inv = 1.f / z;

@@ -227,16 +227,14 @@ __global__ __launch_bounds__(kSumThreads, summary_waves(D)) void summary_kernel(
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       if (nt < wtiles && nt * 16 + 4 * g16 + i < len) m = fmaxf(m, sc[nt][i]);
-  m = fmaxf(m, __shfl_xor(m, 16, kWave));
-  m = fmaxf(m, __shfl_xor(m, 32, kWave));
+  m = col4_max(m);
   float z = 0.f;
 #pragma unroll
   for (int nt = 0; nt < kMaxWidth / 16; ++nt)
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       if (nt < wtiles && nt * 16 + 4 * g16 + i < len) z += expf(sc[nt][i] - m);
-  z += __shfl_xor(z, 16, kWave);
-  z += __shfl_xor(z, 32, kWave);
+  z = col4_sum(z);
   const float delta = m + logf(z);
   const float big = fmaxf(prior, delta);
   const float merged = big + logf(expf(prior - big) + expf(delta - big));
