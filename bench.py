@@ -48,7 +48,7 @@ TRAFFIC = {
     "draft_attention_kernel": (204_226_688, "profiles/draft_attention_kernel_B128_Hq32_Hkv8_raw256.md"),
     "draft_merge_kernel": (77_197_312, "profiles/draft_merge_kernel_B128_Hq32_Hkv8.md"),
     "prefill_kernel + prefill_combine_kernel": (
-        2_758_483_344, "profiles/prefill_kernel_global16_prefill_L5_Hkv8_D128_ctx131072.md"),
+        2_759_473_028, "profiles/prefill_kernel_global16_prefill_L5_Hkv8_D128_ctx131072.md"),
 }
 
 
