@@ -10,6 +10,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <type_traits>
 #include <hip/hip_fp16.h>
 #include <float.h>
 #include <stdint.h>
@@ -178,6 +179,37 @@ __device__ __forceinline__ float row_pair32_max(float v) {
 }
 __device__ __forceinline__ float col4_sum(float v) { return row_pair32_sum(row_pair16_sum(v)); }
 __device__ __forceinline__ float col4_max(float v) { return row_pair32_max(row_pair16_max(v)); }
+
+// Sum over the 64 lanes on VALU cross-lane steps only: DPP quad permutes pair
+// lanes i ^ 1 and i ^ 2; once every group of 4 (then 8) holds one value, the
+// row half-mirror (row mirror) pairs it with group i ^ 4 (i ^ 8); the lane
+// swaps pair rows.  Every lane ends with the total.
+__device__ __forceinline__ double wave_sum_d_dpp(double v) {
+  auto step_dpp = [](double x, auto ctrl_tag) __attribute__((always_inline)) {
+    constexpr int kCtrl = decltype(ctrl_tag)::value;
+    const uint64_t b = static_cast<uint64_t>(__double_as_longlong(x));
+    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(b), kCtrl, 0xf, 0xf, true));
+    const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(b >> 32), kCtrl, 0xf, 0xf, true));
+    return x + __longlong_as_double(static_cast<long long>((static_cast<uint64_t>(hi) << 32) | lo));
+  };
+  v = step_dpp(v, std::integral_constant<int, 0xB1>{});   // quad_perm [1,0,3,2]: lane i ^ 1
+  v = step_dpp(v, std::integral_constant<int, 0x4E>{});   // quad_perm [2,3,0,1]: lane i ^ 2
+  v = step_dpp(v, std::integral_constant<int, 0x141>{});  // row_half_mirror: group of 4 i ^ 4
+  v = step_dpp(v, std::integral_constant<int, 0x140>{});  // row_mirror: group of 8 i ^ 8
+  auto swap = [](double x, bool rows32) __attribute__((always_inline)) {
+    const uint64_t b = static_cast<uint64_t>(__double_as_longlong(x));
+    const uint32_t lo = static_cast<uint32_t>(b), hi = static_cast<uint32_t>(b >> 32);
+    const auto l = rows32 ? __builtin_amdgcn_permlane32_swap(lo, lo, false, false)
+                          : __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
+    const auto h = rows32 ? __builtin_amdgcn_permlane32_swap(hi, hi, false, false)
+                          : __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
+    const double a = __longlong_as_double(static_cast<long long>((static_cast<uint64_t>(h[0]) << 32) | l[0]));
+    const double c = __longlong_as_double(static_cast<long long>((static_cast<uint64_t>(h[1]) << 32) | l[1]));
+    return a + c;
+  };
+  v = swap(v, false);
+  return swap(v, true);
+}
 
 // (value, index) argmax with torch semantics: larger value wins, equal values
 // keep the lower index.

@@ -372,7 +372,7 @@ __global__ __launch_bounds__(kCT) void chain_kernel(ChainArgs a) {
     double t = 0.0;
 #pragma unroll
     for (int k = 0; k < 16; ++k) t += static_cast<double>(x[k]);
-    t = wave_sum_d(t);
+    t = wave_sum_d_dpp(t);
     if (lane == 0) atomic_put_u64(part + c, static_cast<uint64_t>(__double_as_longlong(t)));
   }
   __syncthreads();
