@@ -211,6 +211,29 @@ __device__ __forceinline__ double wave_sum_d_dpp(double v) {
   return swap(v, true);
 }
 
+// Inclusive prefix sum over the 64 lanes on DPP steps only: row shifts by 1, 2,
+// 4 and 8 scan each row of 16 lanes, then the broadcast of lane 15 into rows 1
+// and 3 and of lane 31 into rows 2 and 3 carry the row totals.  Lanes a step
+// does not write, and shifts past a row's start, add 0.
+__device__ __forceinline__ double wave_incl_scan_d_dpp(double v) {
+  auto step = [](double x, auto ctrl_tag, auto row_mask_tag) __attribute__((always_inline)) {
+    constexpr int kCtrl = decltype(ctrl_tag)::value, kRows = decltype(row_mask_tag)::value;
+    const uint64_t b = static_cast<uint64_t>(__double_as_longlong(x));
+    const uint32_t lo =
+        static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(b), kCtrl, kRows, 0xf, true));
+    const uint32_t hi =
+        static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(b >> 32), kCtrl, kRows, 0xf, true));
+    return x + __longlong_as_double(static_cast<long long>((static_cast<uint64_t>(hi) << 32) | lo));
+  };
+  using R = std::integral_constant<int, 0xf>;
+  v = step(v, std::integral_constant<int, 0x111>{}, R{});  // row_shr:1
+  v = step(v, std::integral_constant<int, 0x112>{}, R{});  // row_shr:2
+  v = step(v, std::integral_constant<int, 0x114>{}, R{});  // row_shr:4
+  v = step(v, std::integral_constant<int, 0x118>{}, R{});  // row_shr:8
+  v = step(v, std::integral_constant<int, 0x142>{}, std::integral_constant<int, 0xa>{});  // row_bcast:15
+  return step(v, std::integral_constant<int, 0x143>{}, std::integral_constant<int, 0xc>{});  // row_bcast:31
+}
+
 // (value, index) argmax with torch semantics: larger value wins, equal values
 // keep the lower index.
 struct ArgMax {

@@ -251,6 +251,7 @@ __global__ __launch_bounds__(kST) void finalize_kernel(FinalizeArgs a) {
 constexpr int kCT = 256;        // threads per chain workgroup
 constexpr int kCChunk = 1024;   // elements per chunk: 16 per lane of one wave
 constexpr int kCWaves = kCT / kWave;
+constexpr int kChainRegGroups = 4;  // chunk sums held in registers by the last workgroup: up to 256 chunks
 
 struct ChainArgs {
   const float* p;
@@ -278,22 +279,6 @@ struct ChainArgs {
   int64_t nchunks;
   int slices, cps;    // workgroups per request, chunks per workgroup
 };
-
-__device__ __forceinline__ double wave_incl_scan_d(double v) {
-  const int lane = threadIdx.x & (kWave - 1);
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) {
-    const double t = __shfl_up(v, o, kWave);
-    if (lane >= o) v += t;
-  }
-  return v;
-}
-
-__device__ __forceinline__ double wave_sum_d(double v) {
-#pragma unroll
-  for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-  return v;
-}
 
 // Accepted drafts of request b (every lane returns it): drafted token j
 // (candidates column j + 1) is accepted while u[b, j] * q[b, j, c] < p[b, j, c]
@@ -382,29 +367,60 @@ __global__ __launch_bounds__(kCT) void chain_kernel(ChainArgs a) {
   if (lane == 0) atomic_take_u32(a.arrive + b);  // back to zero for the next call
 
   // The last workgroup: total, then the chunk where the running sum passes
-  // u * total (both walks use the same group-wise scan, so they agree).
+  // u * total (both walks use the same group-wise scans, so they agree).  Up
+  // to kChainRegGroups groups of 64 chunk sums sit in registers, loaded in one
+  // round beside the indices the final writes need.
   auto chunk_sum = [&](int64_t c) -> double {
     return c < a.nchunks ? __longlong_as_double(static_cast<long long>(atomic_peek_u64(part + c))) : 0.0;
   };
-  double total = 0.0;
-  for (int64_t c0 = 0; c0 < a.nchunks; c0 += kWave) {
-    const double inc = wave_incl_scan_d(chunk_sum(c0 + lane));
-    total += __shfl(inc, kWave - 1, kWave);
+  const bool one_pass = len < kWave;
+  int64_t my_slot = 0, my_tok = 0;
+  if (one_pass && lane <= len) {
+    my_slot = ld_idx(a.ridx, a.ridx_dtype, b * a.rsb + static_cast<int64_t>(lane) * a.rsk);
+    if (lane < len) my_tok = ld_idx(a.cand, a.cand_dtype, b * a.csb + static_cast<int64_t>(lane + 1) * a.csk);
   }
-  const double target = static_cast<double>(a.uf[b]) * total;
   int64_t hit_chunk = -1;
-  double base = 0.0;
-  for (int64_t c0 = 0; c0 < a.nchunks; c0 += kWave) {
-    const double x = chunk_sum(c0 + lane);
-    const double inc = wave_incl_scan_d(x);
-    const uint64_t m = __ballot(c0 + lane < a.nchunks && base + inc > target);
-    if (m) {
-      const int l = __ffsll(static_cast<long long>(m)) - 1;
-      hit_chunk = c0 + l;
-      base += __shfl(inc - x, l, kWave);
-      break;
+  double base = 0.0, target;
+  if (a.nchunks <= kWave * kChainRegGroups) {
+    double xs[kChainRegGroups], inc[kChainRegGroups];
+#pragma unroll
+    for (int g = 0; g < kChainRegGroups; ++g) xs[g] = chunk_sum(g * kWave + lane);
+    double total = 0.0;
+#pragma unroll
+    for (int g = 0; g < kChainRegGroups; ++g) {
+      inc[g] = wave_incl_scan_d_dpp(xs[g]);
+      if (g * kWave < a.nchunks) total += __shfl(inc[g], kWave - 1, kWave);
     }
-    base += __shfl(inc, kWave - 1, kWave);
+    target = static_cast<double>(a.uf[b]) * total;
+#pragma unroll
+    for (int g = 0; g < kChainRegGroups; ++g) {
+      const uint64_t m = __ballot(g * kWave + lane < a.nchunks && base + inc[g] > target);
+      if (hit_chunk < 0 && m) {
+        const int l = __ffsll(static_cast<long long>(m)) - 1;
+        hit_chunk = g * kWave + l;
+        base += __shfl(inc[g] - xs[g], l, kWave);
+      }
+      if (hit_chunk < 0) base += __shfl(inc[g], kWave - 1, kWave);
+    }
+  } else {
+    double total = 0.0;
+    for (int64_t c0 = 0; c0 < a.nchunks; c0 += kWave) {
+      const double inc = wave_incl_scan_d_dpp(chunk_sum(c0 + lane));
+      total += __shfl(inc, kWave - 1, kWave);
+    }
+    target = static_cast<double>(a.uf[b]) * total;
+    for (int64_t c0 = 0; c0 < a.nchunks; c0 += kWave) {
+      const double x = chunk_sum(c0 + lane);
+      const double inc = wave_incl_scan_d_dpp(x);
+      const uint64_t m = __ballot(c0 + lane < a.nchunks && base + inc > target);
+      if (m) {
+        const int l = __ffsll(static_cast<long long>(m)) - 1;
+        hit_chunk = c0 + l;
+        base += __shfl(inc - x, l, kWave);
+        break;
+      }
+      base += __shfl(inc, kWave - 1, kWave);
+    }
   }
   int64_t tok = a.vocab - 1;
   if (hit_chunk >= 0) {
@@ -416,7 +432,7 @@ __global__ __launch_bounds__(kCT) void chain_kernel(ChainArgs a) {
       double ls = 0.0;
 #pragma unroll
       for (int e = 0; e < 4; ++e) ls += static_cast<double>(x[4 * i + e]);
-      const double inc = wave_incl_scan_d(ls);
+      const double inc = wave_incl_scan_d_dpp(ls);
       double run = base + (inc - ls);
       int first = -1, lastpos = -1;
 #pragma unroll
@@ -442,11 +458,18 @@ __global__ __launch_bounds__(kCT) void chain_kernel(ChainArgs a) {
     // without an element past it, the chunk's last positive element
     tok = found >= 0 ? found : (last_pos >= 0 ? last_pos : a.vocab - 1);
   }
-  for (int n = lane; n <= len; n += kWave) {
-    const int64_t slot = ld_idx(a.ridx, a.ridx_dtype, b * a.rsb + static_cast<int64_t>(n) * a.rsk);
-    a.aidx[b * a.aisb + static_cast<int64_t>(n) * a.aisk] = static_cast<int32_t>(slot);
-    const int64_t t = n < len ? ld_idx(a.cand, a.cand_dtype, b * a.csb + static_cast<int64_t>(n + 1) * a.csk) : tok;
-    a.predicts[slot] = static_cast<int32_t>(t);
+  if (one_pass) {
+    if (lane <= len) {
+      a.aidx[b * a.aisb + static_cast<int64_t>(lane) * a.aisk] = static_cast<int32_t>(my_slot);
+      a.predicts[my_slot] = static_cast<int32_t>(lane < len ? my_tok : tok);
+    }
+  } else {
+    for (int n = lane; n <= len; n += kWave) {
+      const int64_t slot = ld_idx(a.ridx, a.ridx_dtype, b * a.rsb + static_cast<int64_t>(n) * a.rsk);
+      a.aidx[b * a.aisb + static_cast<int64_t>(n) * a.aisk] = static_cast<int32_t>(slot);
+      const int64_t t = n < len ? ld_idx(a.cand, a.cand_dtype, b * a.csb + static_cast<int64_t>(n + 1) * a.csk) : tok;
+      a.predicts[slot] = static_cast<int32_t>(t);
+    }
   }
   if (lane == 0) a.anum[b] = len;
 }

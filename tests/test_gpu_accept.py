@@ -4,7 +4,8 @@
   probabilities): partial acceptance, an all-accepted request (bonus from the
   last target row), a degenerate residual (p == q: vocab-1), int32 and int64
   index tensors, a permuted ``retrive_index``, rows that are not 16-byte
-  aligned, and the full 151,936 vocabulary.  Accepted lengths, accept
+  aligned, the full 151,936 vocabulary, a 300,007-token vocabulary and a
+  chain of 80 tokens.  Accepted lengths, accept
   indices and accepted tokens bit-exact; the bonus bit-exact except an
   inverse-CDF boundary within 1e-6 of the total (fp64 running sums here,
   fp32 blockwise sums in the reference).
@@ -67,6 +68,8 @@ def misaligned(t):
     (6, 8, 5000, torch.int64, True, False),
     (5, 8, 5001, torch.int32, False, True),
     (3, 16, workloads.VOCAB, torch.int64, True, True),
+    (2, 4, 300_007, torch.int32, True, False),   # more than 256 chunk sums: the looped walk
+    (3, 80, 3000, torch.int64, True, True),      # more than 64 accepted tokens: the looped writes
 ])
 def test_chain_sampling(dev, batch, width, vocab, idx_dtype, aligned, permute):
     p, q, cand, u, uf = chain_inputs(batch, width, vocab, seed=vocab + width)
