@@ -131,27 +131,130 @@ __device__ __forceinline__ void store16_stream(void* p, const float4& v) {
   __builtin_nontemporal_store(v.w, &q->w);
 }
 
+// ------------------------------------------------------ cross-lane ops ---
+//
+// Lane exchanges on VALU operations (DPP and gfx950's lane swaps) rather than
+// LDS permutes (ds_bpermute), so a chain of them waits on no LDS round trip.
+// Like the shuffles they replace, they expect every lane of the wave active.
+
+template <int kCtrl>
+__device__ __forceinline__ uint32_t dpp_mov(uint32_t v) {
+  return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), kCtrl, 0xf, 0xf, false));
+}
+
+// The value lane i ^ kMask holds (kMask = 1, 2, 4, ..., 32): quad permutes for
+// 1 and 2; for 4 the quad reverse (i ^ 3) then the half-row mirror (i ^ 7);
+// for 8 the half-row mirror then the row mirror (i ^ 15); the lane swaps for
+// 16 and 32 (each lane gets both rows of its pair and keeps the other one).
+template <int kMask>
+__device__ __forceinline__ uint32_t lane_xor(uint32_t v) {
+  if constexpr (kMask == 1) {
+    return dpp_mov<0xB1>(v);  // quad_perm [1,0,3,2]
+  } else if constexpr (kMask == 2) {
+    return dpp_mov<0x4E>(v);  // quad_perm [2,3,0,1]
+  } else if constexpr (kMask == 4) {
+    return dpp_mov<0x141>(dpp_mov<0x1B>(v));  // quad_perm [3,2,1,0], row_half_mirror
+  } else if constexpr (kMask == 8) {
+    return dpp_mov<0x140>(dpp_mov<0x141>(v));  // row_half_mirror, row_mirror
+  } else if constexpr (kMask == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return (threadIdx.x & 16) ? r[0] : r[1];
+  } else {
+    static_assert(kMask == 32, "lane_xor: the mask is a power of two below 64");
+    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return (threadIdx.x & 32) ? r[0] : r[1];
+  }
+}
+template <int kMask, typename T>
+__device__ __forceinline__ T lane_xor_as(T v) {
+  if constexpr (sizeof(T) == 4) {
+    return __builtin_bit_cast(T, lane_xor<kMask>(__builtin_bit_cast(uint32_t, v)));
+  } else {
+    static_assert(sizeof(T) == 8, "lane_xor_as: 4- or 8-byte values");
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint64_t lo = lane_xor<kMask>(static_cast<uint32_t>(b));
+    const uint64_t hi = lane_xor<kMask>(static_cast<uint32_t>(b >> 32));
+    return __builtin_bit_cast(T, (hi << 32) | lo);
+  }
+}
+
+// The value of a lane every lane names alike (a wave-uniform lane index).
+template <typename T>
+__device__ __forceinline__ T lane_read(T v, int lane) {
+  if constexpr (sizeof(T) == 4) {
+    return __builtin_bit_cast(T, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+  } else {
+    static_assert(sizeof(T) == 8, "lane_read: 4- or 8-byte values");
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint64_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(b), lane));
+    const uint64_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(b >> 32), lane));
+    return __builtin_bit_cast(T, (hi << 32) | lo);
+  }
+}
+
+// Butterfly over the wave pairing lanes i ^ 32, then i ^ 16, ..., i ^ 1, each
+// step op(own, partner): the operands and order of the shuffle butterfly, so
+// floating-point results are bit-identical to it.  Every lane ends with it.
+template <typename T, typename Op>
+__device__ __forceinline__ T wave_butterfly(T v, Op op) {
+  v = op(v, lane_xor_as<32>(v));
+  v = op(v, lane_xor_as<16>(v));
+  v = op(v, lane_xor_as<8>(v));
+  v = op(v, lane_xor_as<4>(v));
+  v = op(v, lane_xor_as<2>(v));
+  return op(v, lane_xor_as<1>(v));
+}
+
+// Bitonic sort of one 64-bit key per lane across the wave (lane 0 first):
+// descending, or ascending with kAscending.
+template <bool kAscending, int kSize, int kStride>
+__device__ __forceinline__ uint64_t wave_bitonic_steps(uint64_t key) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const uint64_t o = lane_xor_as<kStride>(key);
+  const bool dir = (lane & kSize) == 0 || kSize == kWave;
+  const bool lower = (lane & kStride) == 0;
+  const uint64_t hi = key > o ? key : o, lo = key < o ? key : o;
+  key = (lower == dir) == kAscending ? lo : hi;
+  if constexpr (kStride > 1) {
+    return wave_bitonic_steps<kAscending, kSize, kStride / 2>(key);
+  } else if constexpr (kSize < kWave) {
+    return wave_bitonic_steps<kAscending, kSize * 2, kSize>(key);
+  } else {
+    return key;
+  }
+}
+template <bool kAscending>
+__device__ __forceinline__ uint64_t wave_bitonic_sort(uint64_t key) {
+  return wave_bitonic_steps<kAscending, 2, 1>(key);
+}
+
+// Inclusive prefix sum of 32-bit integers over the wave on DPP steps: row
+// shifts by 1, 2, 4 and 8 scan each row of 16 lanes, then the broadcasts of
+// lane 15 into rows 1 and 3 and of lane 31 into rows 2 and 3 carry the row
+// totals (lanes a step does not write add 0).
+__device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t v) {
+  v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x111, 0xf, 0xf, true));
+  v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x112, 0xf, 0xf, true));
+  v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x114, 0xf, 0xf, true));
+  v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x118, 0xf, 0xf, true));
+  v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x142, 0xa, 0xf, true));
+  v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x143, 0xc, 0xf, true));
+  return v;
+}
+
 // ------------------------------------------------------ wave reductions ---
 
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = kWave / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
-  return v;
+  return wave_butterfly(v, [](float x, float y) __attribute__((always_inline)) { return fmaxf(x, y); });
 }
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-  return v;
+  return wave_butterfly(v, [](float x, float y) __attribute__((always_inline)) { return x + y; });
 }
 __device__ __forceinline__ int wave_max_i(int v) {
-#pragma unroll
-  for (int o = kWave / 2; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o, kWave));
-  return v;
+  return wave_butterfly(v, [](int x, int y) __attribute__((always_inline)) { return max(x, y); });
 }
 __device__ __forceinline__ int wave_sum_i(int v) {
-#pragma unroll
-  for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-  return v;
+  return wave_butterfly(v, [](int x, int y) __attribute__((always_inline)) { return x + y; });
 }
 
 // Reductions over the 4 lanes i, i ^ 16, i ^ 32, i ^ 48 (one column of a

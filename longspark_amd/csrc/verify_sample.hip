@@ -1222,14 +1222,8 @@ __device__ __forceinline__ void wave_sync() {
 }
 
 __device__ __forceinline__ int wave_excl_scan(int v, int* total) {
-  const int lane = threadIdx.x & (kWave - 1);
-  int inc = v;
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) {
-    const int t = __shfl_up(inc, o, kWave);
-    if (lane >= o) inc += t;
-  }
-  *total = __shfl(inc, kWave - 1, kWave);
+  const int inc = static_cast<int>(wave_incl_scan_u32(static_cast<uint32_t>(v)));
+  *total = lane_read(inc, kWave - 1);
   return inc - v;
 }
 
@@ -1330,13 +1324,9 @@ __device__ uint32_t wave_select_kth(WaveShared& ws, int n, int k, bool bf16_keys
       c[j] = ws.hist[4 * lane + j];
       local += c[j];
     }
-    uint32_t suf = local;  // inclusive suffix sum: lanes above own larger digits
-#pragma unroll
-    for (int o = 1; o < kWave; o <<= 1) {
-      const uint32_t v = __shfl_down(suf, o, kWave);
-      if (lane + o < kWave) suf += v;
-    }
-    uint32_t above = suf - local;
+    // lanes above own larger digits: the counts of the lanes past this one
+    const uint32_t pre = wave_incl_scan_u32(local);
+    uint32_t above = lane_read(pre, kWave - 1) - pre;
     int sel = -1, sel_above = 0;
 #pragma unroll
     for (int j = 3; j >= 0; --j) {
@@ -1348,8 +1338,8 @@ __device__ uint32_t wave_select_kth(WaveShared& ws, int n, int k, bool bf16_keys
     }
     const uint64_t who = __ballot(sel >= 0);
     const int src = __ffsll(static_cast<long long>(who)) - 1;
-    const uint32_t d = static_cast<uint32_t>(__shfl(sel, src, kWave));
-    remaining -= __shfl(sel_above, src, kWave);
+    const uint32_t d = static_cast<uint32_t>(lane_read(sel, src));
+    remaining -= lane_read(sel_above, src);
     prefix |= d << shift;
     pmask |= 255u << shift;
     wave_sync();
@@ -1616,21 +1606,12 @@ __device__ RowRec wave_finalize_topk(WaveShared& ws, int count, const Params& p,
       const uint64_t k0 = ws.buf[lane];
       key = cand_key(key_s(k0) / t, key_idx(k0));
     }
-#pragma unroll
-    for (int size = 2; size <= kWave; size <<= 1) {
-#pragma unroll
-      for (int stride = size >> 1; stride > 0; stride >>= 1) {
-        const uint64_t o = __shfl_xor(key, stride, kWave);
-        const bool desc = (lane & size) == 0 || size == kWave;
-        const bool lower = (lane & stride) == 0;
-        key = (lower == desc) ? (key > o ? key : o) : (key < o ? key : o);
-      }
-    }
+    key = wave_bitonic_sort<false>(key);
     wave_sync();
     ws.buf[lane] = key;  // the sorted support keys stay in LDS for the caller
     wave_sync();
     if (n > k) n = k;
-    const float m = n > 0 ? key_s(__shfl(key, 0, kWave)) : -INFINITY;
+    const float m = n > 0 ? key_s(lane_read(key, 0)) : -INFINITY;
     const float e = lane < n ? __expf(key_s(key) - m) : 0.f;
     const float z1 = wave_sum(e);
     const float pi = lane < n ? e / z1 : 0.f;
@@ -1642,7 +1623,7 @@ __device__ RowRec wave_finalize_topk(WaveShared& ws, int count, const Params& p,
     }
     if (p.min_p > 0.f && n_f > 0) {
       const float pp = wave_sum(lane < n_f ? pi : 0.f);
-      const float thr = (__shfl(pi, 0, kWave) / pp) * p.min_p;
+      const float thr = (lane_read(pi, 0) / pp) * p.min_p;
       const uint64_t hit = __ballot(lane < n_f && pi / pp < thr);
       if (hit) n_f = __ffsll(static_cast<long long>(hit)) - 1;
     }
@@ -1657,12 +1638,12 @@ __device__ RowRec wave_finalize_topk(WaveShared& ws, int count, const Params& p,
     rr.n = n_f;
     rr.flags = 0;
     rr.why = 0;
-    const uint64_t lastk = __shfl(key, n_f > 0 ? n_f - 1 : 0, kWave);
+    const uint64_t lastk = lane_read(key, n_f > 0 ? n_f - 1 : 0);
     rr.last = n_f > 0 ? lastk : ~uint64_t(0);
     rr.p_cand = 0.f;
     if (cand_tok >= 0 && cand_by_match) {
       const uint64_t hit = __ballot(lane < n_f && key_idx(key) == cand_tok);
-      const float pv = __shfl(e / zf, hit ? __ffsll(static_cast<long long>(hit)) - 1 : 0, kWave);
+      const float pv = lane_read(e / zf, hit ? __ffsll(static_cast<long long>(hit)) - 1 : 0);
       rr.p_cand = hit ? pv : 0.f;
     } else if (cand_tok >= 0) {
       const float sc = cand_x / t;
@@ -1682,17 +1663,7 @@ __device__ RowRec wave_finalize_topk(WaveShared& ws, int count, const Params& p,
     wave_sync();
     if (n <= kWave) {
       // one key per lane: bitonic sort across the wave, descending
-      uint64_t key = lane < n ? ws.buf[lane] : 0;
-#pragma unroll
-      for (int size = 2; size <= kWave; size <<= 1) {
-#pragma unroll
-        for (int stride = size >> 1; stride > 0; stride >>= 1) {
-          const uint64_t o = __shfl_xor(key, stride, kWave);
-          const bool desc = (lane & size) == 0 || size == kWave;
-          const bool lower = (lane & stride) == 0;
-          key = (lower == desc) ? (key > o ? key : o) : (key < o ? key : o);
-        }
-      }
+      const uint64_t key = wave_bitonic_sort<false>(lane < n ? ws.buf[lane] : 0);
       wave_sync();
       ws.buf[lane] = key;
       wave_sync();
@@ -1717,7 +1688,7 @@ __device__ RowRec wave_finalize_topk(WaveShared& ws, int count, const Params& p,
           n_f = r0 + __ffsll(static_cast<long long>(hit)) - 1;
           break;
         }
-        carry += __shfl(inc, kWave - 1, kWave);
+        carry += lane_read(inc, kWave - 1);
       }
     }
     if (p.min_p > 0.f && n_f > 0) {
@@ -1842,7 +1813,7 @@ __device__ __forceinline__ int accept_length_wave(const Args& a, int64_t b, int*
     const uint64_t fail = __ballot(j < g && !ok);
     if (fail) {
       const int first = __ffsll(static_cast<long long>(fail)) - 1;
-      const int ff = __shfl(fl, first, kWave);
+      const int ff = lane_read(fl, first);
       *flags = (ff & kFlagOverflow) ? ff : 0;
       return base + first;
     }
@@ -1952,13 +1923,13 @@ __device__ __forceinline__ int fused_accept_length(const Args& a, int64_t b, flo
       continue;
     }
     const int k = __ffsll(static_cast<long long>(stop)) - 1;
-    if (!__shfl(static_cast<int>(pub), k, kWave)) {
+    if (!lane_read(static_cast<int>(pub), k)) {
       j = k;
       all = false;
       __builtin_amdgcn_s_sleep(8);
       continue;
     }
-    return __shfl(static_cast<int>(ovf), k, kWave) ? -1 : k;
+    return lane_read(static_cast<int>(ovf), k) ? -1 : k;
   }
   return -1;
 }
@@ -2445,7 +2416,7 @@ __device__ __forceinline__ int resolve_accept_wave(const Args& a, int64_t b, int
   const bool ok = lane < g && !(r.flags & kFlagOverflow) && uv * q < r.p_cand;
   const uint64_t fail = __ballot(lane < g && !ok);
   const int len = fail ? __ffsll(static_cast<long long>(fail)) - 1 : g;
-  const int fl = __shfl(r.flags, len, kWave) & kFlagOverflow;
+  const int fl = lane_read(r.flags, len) & kFlagOverflow;
   if (lane == len) *s_tr = r;
   if (lane == 0) {
     *s_len = len;
@@ -2523,25 +2494,15 @@ __device__ __forceinline__ void resolve_wave(const Args& a, int64_t b, int len, 
     if (a.q_mode == 1 || wave_sum(res) > 1e-8f) val = res;
   }
   // entries in ascending index order (bitonic sort across the wave)
-  uint64_t key = lane < n ? (static_cast<uint64_t>(static_cast<uint32_t>(ti)) << 32) | __float_as_uint(val)
-                          : ~uint64_t(0);
-#pragma unroll
-  for (int size = 2; size <= kWave; size <<= 1) {
-#pragma unroll
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      const uint64_t o = __shfl_xor(key, stride, kWave);
-      const bool asc = (lane & size) == 0 || size == kWave;
-      const bool lower = (lane & stride) == 0;
-      key = (lower == asc) ? (key < o ? key : o) : (key > o ? key : o);
-    }
-  }
+  const uint64_t key = wave_bitonic_sort<true>(
+      lane < n ? (static_cast<uint64_t>(static_cast<uint32_t>(ti)) << 32) | __float_as_uint(val) : ~uint64_t(0));
   const float v = lane < n ? __uint_as_float(static_cast<uint32_t>(key)) : 0.f;
   const float inc = wave_incl_scan_f(v);
-  const float total = __shfl(inc, kWave - 1, kWave);
+  const float total = lane_read(inc, kWave - 1);
   const uint64_t hit = __ballot(lane < n && inc > u * total);
   const int idx = static_cast<int>(key >> 32);
   const int first = hit ? __ffsll(static_cast<long long>(hit)) - 1 : 0;
-  const int at = __shfl(idx, first, kWave);
+  const int at = lane_read(idx, first);
   if (lane == 0) write_result(a, b, len, (total > 0.f && hit) ? at : a.vocab - 1);
 }
 
