@@ -1227,13 +1227,36 @@ __device__ __forceinline__ int wave_excl_scan(int v, int* total) {
   return inc - v;
 }
 
+// Inclusive prefix sum over the wave: at step o (1, 2, ..., 32) lane i adds
+// the value of lane i - o (i >= o), the additions of the shuffle scan in its
+// order, so the sums are bit-identical to it.  Lane i - o is found without LDS
+// permutes: within a row of 16 a row rotation by o, and for the first o lanes
+// of a row the same rotation read from the row before (the lane swaps bring
+// row 0 to row 1 and row 2 to row 3, and row 1 to row 2 by way of rows 0 and 3).
 __device__ __forceinline__ float wave_incl_scan_f(float v) {
   const int lane = threadIdx.x & (kWave - 1);
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) {
-    const float t = __shfl_up(v, o, kWave);
-    if (lane >= o) v += t;
-  }
+  const int j = lane & 15;
+  const bool row2 = (lane >> 4) == 2;
+  auto prev_row = [&](uint32_t x) __attribute__((always_inline)) {
+    const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);  // r[0]: even row, r[1]: odd row
+    const auto s = __builtin_amdgcn_permlane32_swap(r[1], r[1], false, false);  // s[0]: the lower half's
+    return row2 ? s[0] : r[0];
+  };
+  // (every cross-lane operation runs in all lanes; selects pick the results)
+  auto step = [&](auto ror_tag, int o) __attribute__((always_inline)) {
+    const uint32_t u = dpp_mov<decltype(ror_tag)::value>(__float_as_uint(v));  // lane (j - o) mod 16 of the row
+    const uint32_t pu = prev_row(u);
+    const float t = __uint_as_float(j >= o ? u : pu);
+    v = lane >= o ? v + t : v;
+  };
+  step(std::integral_constant<int, 0x121>{}, 1);  // row_ror:1
+  step(std::integral_constant<int, 0x122>{}, 2);  // row_ror:2
+  step(std::integral_constant<int, 0x124>{}, 4);  // row_ror:4
+  step(std::integral_constant<int, 0x128>{}, 8);  // row_ror:8
+  const float t16 = __uint_as_float(prev_row(__float_as_uint(v)));
+  v = lane >= 16 ? v + t16 : v;
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = lane >= 32 ? v + __uint_as_float(r[0]) : v;
   return v;
 }
 
