@@ -75,46 +75,16 @@ struct Race {
   int bi, ok;
 };
 
-template <typename Tag, bool kVec>
-__device__ __forceinline__ void race_tile(const typename Tag::storage* rp, const float* np, int64_t vocab, float t,
-                                          float inv_t, int64_t tile, Race& r) {
-  using S = typename Tag::storage;
+// Fold one tile of 16 entries per lane (x: logits, sq: l / T, n: noise)
+// into the lane's race state, for a tile whose entries are all known finite
+// with valid noise: every validity term is true and left out.
+__device__ __forceinline__ void race_fold_plain(float (&x)[16], const float (&sq)[16], const float (&n)[16],
+                                                int64_t tile, Race& r) {
   const int lane = threadIdx.x & (kWave - 1);
-  float x[16], n[16];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int64_t e0 = tile * kTile + i * (kWave * 4) + lane * 4;
-    if (kVec && e0 + 3 < vocab) {
-      load4<Tag>(rp + e0, x + 4 * i);
-      const uint4 v = load16_stream(np + e0);
-      n[4 * i + 0] = __uint_as_float(v.x);
-      n[4 * i + 1] = __uint_as_float(v.y);
-      n[4 * i + 2] = __uint_as_float(v.z);
-      n[4 * i + 3] = __uint_as_float(v.w);
-    } else {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const bool in = e0 + j < vocab;
-        x[4 * i + j] = in ? to_f32<S>(rp[e0 + j]) : -INFINITY;
-        n[4 * i + j] = in ? np[e0 + j] : 1.f;
-      }
-    }
-  }
   float lm = -INFINITY;
 #pragma unroll
   for (int k = 0; k < 16; ++k) {
-    const float raw = x[k];
-    // l * (1/T) is within 1.5 ulp of the quotient l / T; the exact quotient is
-    // taken where it may overflow, so that validity is decided as the
-    // reference decides it (:97-106)
-    float s = raw * inv_t;
-    if (!(fabsf(s) < 1e37f)) s = raw / t;
-    const bool lvalid = raw == raw && raw != INFINITY;
-    const bool sfin = finite_f(raw) && finite_f(s);
-    const bool svalid = !finite_f(raw) || (s == s && s != INFINITY);
-    const bool nvalid = n[k] > 0.f && n[k] < INFINITY;
-    r.ok &= (lvalid && svalid && (sfin ? nvalid : true)) ? 1 : 0;
-    x[k] = sfin ? s * kLog2e : -INFINITY;
+    x[k] = sq[k] * kLog2e;
     lm = fmaxf(lm, x[k]);
   }
   if (lm > r.m) {  // rescale the running sum to the new maximum
@@ -123,12 +93,10 @@ __device__ __forceinline__ void race_tile(const typename Tag::storage* rp, const
   }
 #pragma unroll
   for (int k = 0; k < 16; ++k) {
-    const bool fin = finite_f(x[k]);
-    r.sum += fin ? __builtin_amdgcn_exp2f(x[k] - r.m) : 0.f;
-    const bool nvalid = n[k] > 0.f && n[k] < INFINITY;
+    r.sum += __builtin_amdgcn_exp2f(x[k] - r.m);
     // log2 of the noise (hardware log2; the noise is clamped to the smallest
     // normal value, below which the instruction does not resolve it)
-    const float lk = (fin && nvalid) ? x[k] - __builtin_amdgcn_logf(fmaxf(n[k], 1.17549435e-38f)) : -INFINITY;
+    const float lk = x[k] - __builtin_amdgcn_logf(fmaxf(n[k], 1.17549435e-38f));
     // entries visit in increasing index order within the lane: strict > keeps the lowest
     if (lk > r.bl) {
       r.bl = lk;
@@ -136,6 +104,111 @@ __device__ __forceinline__ void race_tile(const typename Tag::storage* rp, const
       r.bi = static_cast<int>(tile * kTile + (k >> 2) * (kWave * 4) + lane * 4 + (k & 3));
     }
   }
+}
+
+// The same fold with every validity rule (the reference's :97-106): a NaN or
+// +inf logit, a NaN or +inf l / T of a finite logit, or invalid noise at an
+// entry with a finite scaled logit clears ok; entries without a finite
+// scaled logit take no part.  Runs only for tiles with such entries.
+__device__ __forceinline__ void race_fold_general(float (&x)[16], float (&sq)[16], float (&n)[16], int64_t tile,
+                                               Race& r) {
+  const int lane = threadIdx.x & (kWave - 1);
+  float lm = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const float raw = x[k], s = sq[k];
+    const bool lvalid = raw == raw && raw != INFINITY;
+    const bool sfin = finite_f(raw) && finite_f(s);
+    const bool svalid = !finite_f(raw) || (s == s && s != INFINITY);
+    const bool nvalid = n[k] > 0.f && n[k] < INFINITY;
+    r.ok &= (lvalid && svalid && (sfin ? nvalid : true)) ? 1 : 0;
+    x[k] = sfin ? s * kLog2e : -INFINITY;
+    lm = fmaxf(lm, x[k]);
+    __builtin_amdgcn_sched_barrier(0);  // one entry's lane masks at a time
+  }
+  if (lm > r.m) {
+    r.sum = r.m == -INFINITY ? 0.f : r.sum * __builtin_amdgcn_exp2f(r.m - lm);
+    r.m = lm;
+  }
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const bool fin = finite_f(x[k]);
+    r.sum += fin ? __builtin_amdgcn_exp2f(x[k] - r.m) : 0.f;
+    const bool nvalid = n[k] > 0.f && n[k] < INFINITY;
+    const float lk = (fin && nvalid) ? x[k] - __builtin_amdgcn_logf(fmaxf(n[k], 1.17549435e-38f)) : -INFINITY;
+    if (lk > r.bl) {
+      r.bl = lk;
+      r.bs = x[k];
+      r.bi = static_cast<int>(tile * kTile + (k >> 2) * (kWave * 4) + lane * 4 + (k & 3));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+template <typename Tag, bool kVec>
+__device__ __forceinline__ void race_tile(const typename Tag::storage* rp, const float* np, int64_t vocab, float t,
+                                          float inv_t, int64_t tile, Race& r) {
+  using S = typename Tag::storage;
+  const int lane = threadIdx.x & (kWave - 1);
+  float x[16], n[16];
+  auto load_vec = [&](int i, int64_t e0) __attribute__((always_inline)) {
+    load4<Tag>(rp + e0, x + 4 * i);
+    const uint4 v = load16_stream(np + e0);
+    n[4 * i + 0] = __uint_as_float(v.x);
+    n[4 * i + 1] = __uint_as_float(v.y);
+    n[4 * i + 2] = __uint_as_float(v.z);
+    n[4 * i + 3] = __uint_as_float(v.w);
+  };
+  if (kVec && (tile + 1) * kTile <= vocab) {
+    // a whole tile inside the row: no per-vector bounds checks
+#pragma unroll
+    for (int i = 0; i < 4; ++i) load_vec(i, tile * kTile + i * (kWave * 4) + lane * 4);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t e0 = tile * kTile + i * (kWave * 4) + lane * 4;
+      if (kVec && e0 + 3 < vocab) {
+        load_vec(i, e0);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const bool in = e0 + j < vocab;
+          x[4 * i + j] = in ? to_f32<S>(rp[e0 + j]) : -INFINITY;
+          n[4 * i + j] = in ? np[e0 + j] : 1.f;
+        }
+      }
+    }
+  }
+  // l * (1/T) is within 1.5 ulp of the quotient l / T; the exact quotient is
+  // taken where the product may overflow (or is NaN), so that validity is
+  // decided as the reference decides it (:97-106).  That is rare: the
+  // divisions run only in a wave with such an entry.
+  float sq[16];
+  bool slow = false;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    sq[k] = x[k] * inv_t;
+    slow |= !(fabsf(sq[k]) < 1e37f);
+  }
+  if (__builtin_expect(__ballot(slow) != 0, 0)) {
+#pragma unroll
+    for (int k = 0; k < 16; ++k)
+      if (!(fabsf(sq[k]) < 1e37f)) sq[k] = x[k] / t;
+  }
+  // A tile whose entries all have a finite logit, a finite product l * (1/T)
+  // and noise in (0, inf) takes the fold without validity selects: x * 0 is
+  // exactly 0 for finite x, so one fused sum per entry finds an infinity or a
+  // NaN among logit, scaled logit and noise (a sum that overflows only sends
+  // the tile to the general fold).
+  float chk = 0.f, nmin = INFINITY;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    chk = fmaf(x[k] + sq[k] + n[k], 0.f, chk);
+    nmin = fminf(nmin, n[k]);
+  }
+  const bool plain = !slow && chk == 0.f && nmin > 0.f;
+  if (__builtin_expect(__ballot(!plain) == 0, 1)) race_fold_plain(x, sq, n, tile, r);
+  else race_fold_general(x, sq, n, tile, r);
 }
 
 // Merge (m, sum, best) of two parts: the larger maximum, both sums rescaled
@@ -239,6 +312,30 @@ __global__ __launch_bounds__(kSS) void sample_step_kernel(SampleArgs a) {
 inline uint64_t ss_up256(uint64_t x) { return (x + 255) & ~uint64_t(255); }
 inline int64_t ss_tiles(int64_t vocab) { return (vocab + kTile - 1) / kTile; }
 
+// Workgroups of a sample-step kernel resident on the current device at once:
+// CUs x the per-CU count its compiled registers and LDS allow (queried once
+// per kernel).
+int64_t resident_workgroups(void (*kern)(SampleArgs)) {
+  static void (*seen[8])(SampleArgs) = {};
+  static int64_t count[8] = {};
+  for (int i = 0; i < 8; ++i)
+    if (seen[i] == kern) return count[i];
+  int dev = 0, cus = 0, per_cu = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    cus = 256;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kSS, 0) != hipSuccess || per_cu <= 0) per_cu = 4;
+  (void)hipGetLastError();
+  const int64_t n = static_cast<int64_t>(cus) * per_cu;
+  for (int i = 0; i < 8; ++i)
+    if (!seen[i]) {
+      seen[i] = kern;
+      count[i] = n;
+      break;
+    }
+  return n;
+}
+
 }  // namespace
 }  // namespace ls
 
@@ -279,30 +376,31 @@ extern "C" int ls_sample_step(const void* logits, int32_t logits_dtype, int64_t 
   a.arrive = static_cast<uint32_t*>(counters);
   a.part = static_cast<uint64_t*>(scratch);
   a.ntiles = ss_tiles(vocab);
-  // tps = tiles per wave: about 1,792 workgroups (one resident round at seven
-  // 4-wave workgroups per CU), each wave streaming a contiguous range
-  const int64_t want_waves = 1792 * kSSWaves;
-  int64_t tpw = (rows * a.ntiles + want_waves - 1) / want_waves;
-  if (tpw < 1) tpw = 1;
-  a.tps = static_cast<int>(tpw);
-  a.slices = static_cast<int>((a.ntiles + kSSWaves * tpw - 1) / (kSSWaves * tpw));
-  LS_CHECK(rows * a.slices < (int64_t(1) << 31), LS_ERR_SHAPE, "ls_sample_step: rows x vocab too large for one launch");
-  const dim3 grid(static_cast<unsigned>(rows * a.slices));
-  hipStream_t st = static_cast<hipStream_t>(stream);
+  // the kernel for this dtype and alignment
   const bool nvec = aligned16(exp_noise) && noise_row_stride % 4 == 0;
+  void (*kern)(SampleArgs) = nullptr;
 #define LS_SS(TAG)                                                                                            \
   do {                                                                                                        \
     using S = typename TAG::storage;                                                                          \
     const bool vec = nvec && (reinterpret_cast<uintptr_t>(logits) % (4 * sizeof(S))) == 0 &&                  \
                      logits_row_stride % 4 == 0;                                                              \
-    if (vec) sample_step_kernel<TAG, true><<<grid, kSS, 0, st>>>(a);                                          \
-    else sample_step_kernel<TAG, false><<<grid, kSS, 0, st>>>(a);                                             \
+    kern = vec ? sample_step_kernel<TAG, true> : sample_step_kernel<TAG, false>;                              \
   } while (0)
   if (logits_dtype == LS_F32) LS_SS(F32);
   else if (logits_dtype == LS_BF16) LS_SS(BF16);
   else if (logits_dtype == LS_F16) LS_SS(F16);
   else return fail(LS_ERR_DTYPE, "ls_sample_step: logits must be fp32, bf16 or fp16");
 #undef LS_SS
+  // tps = tiles per wave: as many workgroups as are resident at once (one
+  // round), each wave streaming a contiguous range
+  const int64_t want_waves = resident_workgroups(kern) * kSSWaves;
+  int64_t tpw = (rows * a.ntiles + want_waves - 1) / want_waves;
+  if (tpw < 1) tpw = 1;
+  a.tps = static_cast<int>(tpw);
+  a.slices = static_cast<int>((a.ntiles + kSSWaves * tpw - 1) / (kSSWaves * tpw));
+  LS_CHECK(rows * a.slices < (int64_t(1) << 31), LS_ERR_SHAPE, "ls_sample_step: rows x vocab too large for one launch");
+  const dim3 grid(static_cast<unsigned>(rows * a.slices));
+  hipLaunchKernelGGL(kern, grid, dim3(kSS), 0, static_cast<hipStream_t>(stream), a);
   LS_LAUNCH_CHECK();
   return LS_OK;
 }
