@@ -43,7 +43,7 @@ constexpr int kVR = (kBlk / 2) * kChunks / kMinThreads;   // value pairs per thr
 constexpr int kKB = kD / 32;
 constexpr int kDB = kD / 16;
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr size_t kLds = static_cast<size_t>(kBlk) * kKP * 2 + static_cast<size_t>(kD) * kVP * 2;
+constexpr size_t kLds = static_cast<size_t>(kBlk) * kKP * 2 + static_cast<size_t>(kD) * kVP * 2 + kRaw * 4;
 
 __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
   typedef __attribute__((ext_vector_type(2))) float f32x2;
@@ -121,6 +121,7 @@ __global__ __launch_bounds__(1024) void draft_attention_kernel(const ls_draft_at
   extern __shared__ __align__(16) char smem[];
   uint16_t* kls = reinterpret_cast<uint16_t*>(smem);
   uint16_t* vls = kls + kBlk * kKP;
+  int32_t* locs = reinterpret_cast<int32_t*>(vls + kD * kVP);  // the request's window rows
 
   const int64_t b = blockIdx.x / a.kv_heads;
   const int kvh = static_cast<int>(blockIdx.x % a.kv_heads);
@@ -155,7 +156,13 @@ __global__ __launch_bounds__(1024) void draft_attention_kernel(const ls_draft_at
   raw_len = raw_len < 0 ? 0 : (raw_len > kRaw ? kRaw : raw_len);
   const char* kbase = static_cast<const char*>(a.key_cache) + kvh * a.kc_stride_h * 2;
   const char* vbase = static_cast<const char*>(a.value_cache) + kvh * a.vc_stride_h * 2;
-  const int32_t* pt = a.page_table + b * a.pt_stride_b;
+  // The window's row locations, read once into LDS, so each block's loads
+  // wait on no page-table round trip.
+  {
+    const int32_t* pt = a.page_table + b * a.pt_stride_b;
+    for (int i = tid; i < raw_len; i += nthr) locs[i] = pt[i];
+  }
+  lds_barrier();
   for (int tb = 0; tb < raw_len; tb += kBlk) {
     // loads first (no branch around them; rows past the window read row
     // raw_len - 1 and get weight 0), then the LDS stores
@@ -163,7 +170,7 @@ __global__ __launch_bounds__(1024) void draft_attention_kernel(const ls_draft_at
 #pragma unroll
     for (int i = 0; i < kKR; ++i) {
       const int j = min(i * nthr + tid, kBlk * kChunks - 1);
-      const int64_t loc = pt[min(tb + j / kChunks, raw_len - 1)];
+      const int64_t loc = locs[min(tb + j / kChunks, raw_len - 1)];
       kr[i] = load16_global(kbase + (loc * a.kc_stride_s + (j % kChunks) * 8) * 2);
     }
 #pragma unroll
@@ -172,7 +179,7 @@ __global__ __launch_bounds__(1024) void draft_attention_kernel(const ls_draft_at
       const int p2 = v % (kBlk / 2), c = v / (kBlk / 2);
 #pragma unroll
       for (int e = 0; e < 2; ++e) {
-        const int64_t loc = pt[min(tb + 2 * p2 + e, raw_len - 1)];
+        const int64_t loc = locs[min(tb + 2 * p2 + e, raw_len - 1)];
         vr[i][e] = load16_global(vbase + (loc * a.vc_stride_s + c * 8) * 2);
       }
     }
