@@ -42,9 +42,9 @@ TRAFFIC = {
     "window_gather_kernel": (604_552_647, "profiles/window_gather_kernel_B8_L36_Hkv8_D128_ctx131072.md"),
     "summary_kernel": (646_838_203, "profiles/summary_kernel_B8_L36_R256_W16.md"),
     "softmax_temp_resident_kernel": (1_868_715_744, "profiles/softmax_temp_resident_kernel_B128_K16_V151936.md"),
-    "chain_kernel": (158_497_097, "profiles/chain_kernel_chain_sampling_B128_K16_V151936.md"),
+    "chain_kernel": (158_529_676, "profiles/chain_kernel_chain_sampling_B128_K16_V151936.md"),
     "request_bias_kernel": (1_403_662_037, "profiles/request_bias_kernel_adjust_logits_B128_K16_V151936.md"),
-    "sample_step_kernel": (156_653_721, "profiles/sample_step_kernel_B128_V151936.md"),
+    "sample_step_kernel": (156_502_794, "profiles/sample_step_kernel_B128_V151936.md"),
     "draft_attention_kernel": (204_226_688, "profiles/draft_attention_kernel_B128_Hq32_Hkv8_raw256.md"),
     "draft_merge_kernel": (77_197_312, "profiles/draft_merge_kernel_B128_Hq32_Hkv8.md"),
     "prefill_kernel + prefill_combine_kernel": (
