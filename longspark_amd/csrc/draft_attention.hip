@@ -293,8 +293,17 @@ __device__ __forceinline__ float row_sum4(float v) { return col4_sum(v); }
 
 // kMaxThreads bounds the workgroup (64 x query heads per KV head); the
 // smaller bounds leave the compiler registers for the loads issued up front.
+// Up to 4 query heads per KV head the summary state rows (16 x 128 fp32 per
+// head) go straight from memory to LDS (global_load_lds), so they hold no
+// registers while the wave waits; the kernel then fits 4 waves per SIMD and
+// 4,096 waves run in one residency round.
 template <int kMaxThreads>
-__global__ __launch_bounds__(kMaxThreads) void draft_merge_kernel(const ls_draft_attention_args a) {
+constexpr int merge_waves_per_simd() { return kMaxThreads <= 256 ? 4 : 1; }
+template <int kMaxThreads>
+__global__ __launch_bounds__(kMaxThreads, merge_waves_per_simd<kMaxThreads>()) void draft_merge_kernel(
+    const ls_draft_attention_args a) {
+  constexpr bool kStateLds = kMaxThreads <= 256;
+  __shared__ float state_lds[kStateLds ? (kMaxThreads / kWave) * kGlobal * kD : 1];
   const int64_t b = blockIdx.x / a.kv_heads;
   const int kvh = static_cast<int>(blockIdx.x % a.kv_heads);
   const int groups = a.q_heads / a.kv_heads;
@@ -364,14 +373,29 @@ __global__ __launch_bounds__(kMaxThreads) void draft_merge_kernel(const ls_draft
     }
   }
   // summary state rows 4*g16 .. 4*g16+3, column db*16 + c16 (fp32, rounded to bf16 as they are packed)
-  float gvr[kDB][4];
+  float gvr[kStateLds ? 1 : kDB][4];
+  float* sl = state_lds + (kStateLds ? wave * kGlobal * kD : 0);
   {
     const int64_t slot = a.state_slots[b];
-    const float* gv = a.global_values + slot * a.gv_stride_b + head * a.gv_stride_h + (4 * g16) * a.gv_stride_g + c16;
+    const float* gv = a.global_values + slot * a.gv_stride_b + head * a.gv_stride_h;
+    if constexpr (kStateLds) {
+      // LDS word r * 128 + (col ^ 16 * (r >> 2)) holds (row r, col): the reads
+      // below (rows 4*g16 + i, columns db*16 + c16) then fall on 64 distinct
+      // banks.  Load j fills words j*64 .. j*64+63: row j/2, one half of it.
 #pragma unroll
-    for (int db = 0; db < kDB; ++db)
+      for (int j = 0; j < kGlobal * kD / kWave; ++j) {
+        const int r = j >> 1;
+        const int col = (((j & 1) << 6) | lane) ^ (16 * (r >> 2));
+        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(gv + r * a.gv_stride_g + col),
+                                         (__attribute__((address_space(3))) void*)(sl + j * kWave), 4, 0, 0);
+      }
+    } else {
+      const float* g = gv + (4 * g16) * a.gv_stride_g + c16;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) gvr[db][i] = gv[i * a.gv_stride_g + db * 16];
+      for (int db = 0; db < kDB; ++db)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) gvr[db][i] = g[i * a.gv_stride_g + db * 16];
+    }
   }
   if (!row_ok) {
     // q rows past 7 take part in no product's output row, but the tile
@@ -446,11 +470,16 @@ __global__ __launch_bounds__(kMaxThreads) void draft_merge_kernel(const ls_draft
   // one reciprocal per normaliser: x * (1/z) is within one fp32 ulp of x / z, far inside the bf16 output
   const float inv_gz = 1.f / gz, inv_lz = 1.f / lz, inv_norm = 1.f / norm;
   uint16_t* out = static_cast<uint16_t*>(a.output) + b * a.o_stride_b + head * a.o_stride_h + row * a.o_stride_r;
+  // the state rows' LDS writes are counted with the wave's other loads
+  if constexpr (kStateLds) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 #pragma unroll
   for (int db = 0; db < kDB; ++db) {
     const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
-    const f32x4_t go = Mma<BF16>::run(
-        make_uint4(pack_bf16(gvr[db][0], gvr[db][1]), pack_bf16(gvr[db][2], gvr[db][3]), 0u, 0u), gpb, zero);
+    float g4[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      g4[i] = kStateLds ? sl[(4 * g16 + i) * kD + ((db * 16 + c16) ^ (16 * g16))] : gvr[kStateLds ? 0 : db][i];
+    const f32x4_t go = Mma<BF16>::run(make_uint4(pack_bf16(g4[0], g4[1]), pack_bf16(g4[2], g4[3]), 0u, 0u), gpb, zero);
     const f32x4_t lo = Mma<BF16>::run(make_uint4(lvp[db][0], lvp[db][1], 0u, 0u), lpb, zero);
     const uint2 rv = rov[db];
     const float r4[4] = {bf16_lo(rv.x), bf16_hi(rv.x), bf16_lo(rv.y), bf16_hi(rv.y)};
