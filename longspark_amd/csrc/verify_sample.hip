@@ -2054,18 +2054,29 @@ struct MergeShared {
 // the slices' own k-th values) are kept.  Wave 0 then keeps the row's k
 // largest and writes the row record and support; the record is returned in
 // wave 0.
+constexpr int kMergeLanes = kT / kDraftSlices;         // threads per slice in the merge
+constexpr int kMergePer = kDraftCap / kMergeLanes;     // hand-off entries per thread
+
+// The thread's share of request b's slice hand-offs (entries part + kMergeLanes
+// * u of slice tid / kMergeLanes), requested before the acceptance is known:
+// the addresses do not depend on it, and entries past a slice's count are
+// ignored by the merge.
+__device__ __forceinline__ void draft_merge_prefetch(const Args& a, int64_t b, uint64_t (&v)[kMergePer]) {
+  const int sl = threadIdx.x / kMergeLanes, part = threadIdx.x % kMergeLanes;
+  const uint64_t* src = a.pub_d + b * kNBuf + static_cast<int64_t>(sl) * kDraftCap + part;
+#pragma unroll
+  for (int u = 0; u < kMergePer; ++u) v[u] = src[kMergeLanes * u];
+}
+
 __device__ __forceinline__ RowRec draft_merge_block(const Args& a, WaveShared& ws, MergeShared& ms, int64_t b,
-                                                    const Params& p, float slice_bound, float raw_max) {
-  constexpr int kLanes = kT / kDraftSlices;
-  constexpr int kPer = kDraftCap / kLanes;
+                                                    const Params& p, float slice_bound, float raw_max,
+                                                    const uint64_t (&v)[kMergePer]) {
+  constexpr int kLanes = kMergeLanes;
+  constexpr int kPer = kMergePer;
   static_assert(kLanes * kDraftSlices == kT && kPer * kLanes == kDraftCap, "merge lane layout");
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wid = tid / kWave;
   const int sl = tid / kLanes, part = tid % kLanes;
   const int my_n = (ms.cnt[sl] - part + kLanes - 1) / kLanes;  // entries part + kLanes * t
-  const uint64_t* src = a.pub_d + b * kNBuf + static_cast<int64_t>(sl) * kDraftCap + part;
-  uint64_t v[kPer];
-#pragma unroll
-  for (int u = 0; u < kPer; ++u) v[u] = src[kLanes * max(min(u, my_n - 1), 0)];
   float t0 = -INFINITY, t1 = -INFINITY;
 #pragma unroll
   for (int u = 0; u < kPer; ++u) {
@@ -2586,6 +2597,9 @@ __global__ __launch_bounds__(kT) void resolve_kernel(Args a) {
   if (a.fuse_draft && tid < a.width) atomic_take_u64(a.acc_t + b * a.width + tid);
   if (a.p_cand_out)
     for (int j = tid; j < g; j += kT) a.p_cand_out[b * g + j] = a.rec_t[b * a.width + j].p_cand;
+  // The slices' hand-offs, requested first (see draft_merge_prefetch).
+  uint64_t pre[kMergePer];
+  if (a.q_mode == 0 && a.dwave) draft_merge_prefetch(a, b, pre);
   // Wave 0: the accepted length, and whether the draft row at the rejection
   // is merged from wavefront slices (1), listed bad by a slice (2), or not;
   // the target support at the accepted length is requested meanwhile.
@@ -2651,7 +2665,7 @@ __global__ __launch_bounds__(kT) void resolve_kernel(Args a) {
   RowRec dm{};  // the merged draft record (wave 0)
   const int merge = s_merge;
   if (merge == 1) {
-    dm = draft_merge_block(a, ws, ms, b, draft_params(a, b), s_sbound, s_rawmax);
+    dm = draft_merge_block(a, ws, ms, b, draft_params(a, b), s_sbound, s_rawmax, pre);
   } else if (merge == 2 && tid < kWave) {
     dm = wave_finalize_topk(ws, 0, draft_params(a, b), s_rawmax, kWhyMerge, a.rec_d + b, a.sidx_d + b * kCap,
                             a.sp_d + b * kCap, -1, NAN, a.list_cnt + 1, a.list_d, static_cast<int32_t>(b));
