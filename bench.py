@@ -46,7 +46,7 @@ TRAFFIC = {
     "request_bias_kernel": (1_403_662_037, "profiles/request_bias_kernel_adjust_logits_B128_K16_V151936.md"),
     "sample_step_kernel": (156_502_794, "profiles/sample_step_kernel_B128_V151936.md"),
     "draft_attention_kernel": (204_226_688, "profiles/draft_attention_kernel_B128_Hq32_Hkv8_raw256.md"),
-    "draft_merge_kernel": (77_197_312, "profiles/draft_merge_kernel_B128_Hq32_Hkv8.md"),
+    "draft_merge_kernel": (77_205_083, "profiles/draft_merge_kernel_B128_Hq32_Hkv8.md"),
     "prefill_kernel + prefill_combine_kernel": (
         2_759_473_028, "profiles/prefill_kernel_global16_prefill_L5_Hkv8_D128_ctx131072.md"),
 }
