@@ -1416,14 +1416,18 @@ __device__ void wave_sort_desc(WaveShared& ws, int n) {
 
 // Transform what is pending, then keep the k largest (within the rounding
 // margin); returns the new raw threshold (or -FLT_MAX if n <= k).  kth (if
-// given) gets the k-th largest value (ties counted) when n > k.
+// given) gets, when n > k, the k-th largest value (ties counted) for bf16
+// keys and its top 16 bits for other keys: never above the k-th largest.
 __device__ __forceinline__ float wave_compact_topk(WaveShared& ws, const XForm& f, int& count, int& ntrans, int k,
                                                   bool bf16_raw, float* kth = nullptr) {
   wave_transform(ws, f, ntrans, count);
   ntrans = count;
   if (count <= k) return -FLT_MAX;
-  // penalties change values; the mask only sets -inf (a bf16 value)
-  const float xk = unordered_f32(wave_select_kth(ws, count, k, bf16_raw && !f.pbits));
+  // penalties change values; the mask only sets -inf (a bf16 value).  Other
+  // keys get the k-th largest's top 16 bits (a value no larger): the margin
+  // below keeps every candidate of the k largest either way.
+  const bool bf16_keys = bf16_raw && !f.pbits;
+  const float xk = unordered_f32(wave_select_kth(ws, count, k, bf16_keys, !bf16_keys));
   if (kth) *kth = xk;
   const float thr = x_lower(xk);
   count = wave_compact_ge(ws, count, ordered_f32(thr));
@@ -1501,7 +1505,8 @@ __device__ __forceinline__ void wave_scan_candidates(WaveShared& ws, const typen
       }
     }
     const uint32_t o[4] = {ordered_f32(t0), ordered_f32(t1), ordered_f32(t2), ordered_f32(t3)};
-    const float tk = unordered_f32(wave_kth_ballot<4>(o, k, 0));
+    // top 16 bits of the k-th largest (a value no larger, so still a bound)
+    const float tk = unordered_f32(wave_kth_ballot<4>(o, k, 16));
     if (tk > -INFINITY) tau = x_lower(tk);
   }
 
