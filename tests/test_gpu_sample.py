@@ -2,8 +2,9 @@
 
 Rows of fp32 and bf16 logits at the full 151,936 vocabulary (vector path),
 an odd vocabulary with a row stride wider than it (element path), masked
-(-inf) entries, per-row temperatures, invalid rows, and the workspace path
-that draws its own noise.  Tokens bit-exact except where the two largest keys
+(-inf) entries, per-row temperatures, invalid rows, scaled logits near the
+float range (the exact-quotient path), and the workspace path that draws its
+own noise.  Tokens bit-exact except where the two largest keys
 p / E lie within 1e-6 of each other (fp64 keys); q within 1e-5 relative of the
 fp64 value of p at the kernel's token.
 """
@@ -75,6 +76,29 @@ def test_sample_step_invalid_rows(dev):
     with pytest.raises(RuntimeError, match="invalid probability row"):
         sample.sample_step_tokens_with_q(step_logits=x.to(dev), temperatures=temps.to(dev),
                                          exp_noise=noise.to(dev), check=True)
+
+
+def test_sample_step_scaled_logit_near_the_float_range(dev):
+    """Entries whose product l * (1/T) reaches 1e37 take the exact quotient l / T
+    (only in the wave that holds them): a huge finite scaled logit stays valid
+    and wins its row, one that overflows makes the row invalid."""
+    vocab = workloads.VOCAB
+    g = torch.Generator().manual_seed(11)
+    x = 3.0 * torch.randn(3, vocab, generator=g)
+    x[0, 1234] = 2.0e37          # l / T = 2.2e37: finite, far above every other entry
+    x[1, 5] = 3.0e38             # l / T = 6e38: +inf, an invalid row
+    temps = torch.tensor([0.9, 0.5, 1.1])
+    noise = torch.empty(3, vocab).exponential_(1, generator=g)
+    print("sample_step scaled logits near the float range", flush=True)
+    tokens, q = sample.sample_step_tokens_with_q(step_logits=x.to(dev), temperatures=temps.to(dev),
+                                                 exp_noise=noise.to(dev))
+    torch.cuda.synchronize()
+    tok_r, q_r, valid = ov.sample_step_tokens_with_q(x, temps, noise)
+    assert valid.tolist() == [True, False, True]
+    tokens, q = tokens.cpu(), q.cpu()
+    assert int(tokens[0]) == 1234 and int(tok_r[0]) == 1234 and abs(float(q[0]) - 1.0) <= 1e-6
+    assert int(tokens[1]) == 0 and bool(torch.isnan(q[1]))
+    check(x[2:], temps[2:], noise[2:], tokens[2:], q[2:])
 
 
 def test_sample_step_workspace_draws_noise(dev):
