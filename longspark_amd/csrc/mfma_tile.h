@@ -28,6 +28,19 @@ struct Mma<F16> {
   }
 };
 
+// Four 16-bit values of one column from four consecutive rows of a row-major
+// LDS tile, through gfx950's transposing LDS read (ds_read_b64_tr_b16).  In
+// each group of 16 lanes, lane L passes the address of the 8 bytes at (row0 +
+// L / 4, col0 + 4 * (L % 4)); lane i of the group receives column col0 + i of
+// rows row0 .. row0 + 3 (row0 first).  This is the operand layout of a
+// 16x16x32 product's A rows read from a [rows][cols] tile, with no transposed
+// copy in LDS.
+__device__ __forceinline__ uint2 lds_read_col4(const uint16_t* piece) {
+  typedef short v4i16 __attribute__((ext_vector_type(4)));
+  const v4i16 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16*)(piece));
+  return __builtin_bit_cast(uint2, r);
+}
+
 __device__ __forceinline__ const char* layer_base(const ls_kv_rows& r, int layer) {
   return r.layers ? reinterpret_cast<const char*>(r.layers[layer])
                   : static_cast<const char*>(r.base) + static_cast<int64_t>(layer) * r.stride_layer * 2;

@@ -16,10 +16,11 @@
 // main kernel finishes the rows itself.
 //
 // Per 32-token step (64 for head_dim 64):
-//   staging  K rows -> LDS as they are ([token][d]); V rows -> LDS transposed
-//            ([d][token], two tokens per 4-byte write) so that a lane's A
-//            operand of the P.V product is two 8-byte reads.  The rows of the
-//            next two steps are in flight in registers while a step computes.
+//   staging  K and V rows -> LDS as they are ([token][d], 16-byte writes);
+//            a lane's A operand of the P.V product (4 tokens x 2 of one d
+//            column) is two transposing 8-byte reads (ds_read_b64_tr_b16).
+//            The rows of the next two steps are in flight in registers while
+//            a step computes.
 //            The tile's query rows sit in LDS for the whole split.
 //   scores   S^T[16 tok x 16 rows] = K[16 x D] . Q^T[D x 16]   (16x16x32 MFMA);
 //            the lane holding row c16 gets tokens 4*g16 + i of each tile.
@@ -47,7 +48,9 @@ struct PrefillShape {
   static constexpr int kKP = D + 16;                  // 16-bit elements per LDS key / query row: a 32-byte skew per
                                                       // row keeps a 16-lane x 16-byte row read on distinct banks of
                                                       // gfx950's 64-bank LDS (D + 8 stalled 25% of LDS cycles)
-  static constexpr int kVP = kBlk + 4;                // 16-bit elements per LDS transposed value row
+  static constexpr int kVRP = D + 16;                 // 16-bit elements per LDS value row (token-major, skewed as
+                                                      // the key rows, so a transposing read of 16 rows x 32
+                                                      // bytes falls on each bank twice)
   static constexpr int kChunks = D / 8;               // 16-byte vectors per row
   static constexpr int kKVecs = kBlk * kChunks;       // key vectors per step
   static constexpr int kVUnits = (kBlk / 2) * kChunks;  // value units (2 tokens x 8 d) per step
@@ -56,7 +59,7 @@ struct PrefillShape {
   static constexpr int kNT = kBlk / 16;               // 16-token score tiles per step
   static constexpr int kKB = D / 32;                  // 32-deep steps of the score product
   static constexpr int kDB = D / 16;                  // 16-wide column blocks of the output
-  static constexpr size_t kLds = static_cast<size_t>(kBlk) * kKP * 2 + static_cast<size_t>(D) * kVP * 2;
+  static constexpr size_t kLds = static_cast<size_t>(kBlk) * kKP * 2 + static_cast<size_t>(kBlk) * kVRP * 2;
 };
 
 struct PrefillGeom {
@@ -97,12 +100,6 @@ __device__ __forceinline__ int table_loc(const ls_prefill_args& a, int64_t b, in
 __device__ __forceinline__ int clamp_len(const ls_prefill_args& a, int64_t b) {
   const int64_t l = a.seq_lens[b];
   return static_cast<int>(l < 0 ? 0 : (l > a.max_len ? a.max_len : l));
-}
-
-// 16-bit element e (0..7) of a 16-byte vector
-__device__ __forceinline__ uint32_t half_of(const uint4& v, int e) {
-  const uint32_t w = e < 2 ? v.x : (e < 4 ? v.y : (e < 6 ? v.z : v.w));
-  return (e & 1) ? (w >> 16) : (w & 0xffffu);
 }
 
 template <int D, typename Tag, bool kCap>
@@ -163,7 +160,7 @@ __device__ __forceinline__ void prefill_body(const ls_prefill_args& a, const Pre
 
   // Query rows of this tile -> LDS (pitch kKP); each wave reads its rows as
   // the B operand of S^T (depth kb*32 + 8*g16 .. +7).
-  uint16_t* qls = vls + D * Sh::kVP;
+  uint16_t* qls = vls + kBlk * Sh::kVRP;
   const int tile_rows = min(nrows - tile * kMaxRowsPerTile, kMaxRowsPerTile);
   for (int j = tid; j < tile_rows * Sh::kChunks; j += nthr) {
     const int rl = j / Sh::kChunks, c = j % Sh::kChunks;
@@ -225,10 +222,8 @@ __device__ __forceinline__ void prefill_body(const ls_prefill_args& a, const Pre
       const int v = i * nthr + tid;
       if (v < Sh::kVUnits) {
         const int p2 = v % (kBlk / 2), c = v / (kBlk / 2);
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-          *reinterpret_cast<uint32_t*>(vls + (c * 8 + e) * Sh::kVP + 2 * p2) =
-              half_of(R.v[i][0], e) | (half_of(R.v[i][1], e) << 16);
+        *reinterpret_cast<uint4*>(vls + (2 * p2) * Sh::kVRP + c * 8) = R.v[i][0];
+        *reinterpret_cast<uint4*>(vls + (2 * p2 + 1) * Sh::kVRP + c * 8) = R.v[i][1];
       }
     }
   };
@@ -301,9 +296,10 @@ __device__ __forceinline__ void prefill_body(const ls_prefill_args& a, const Pre
       pb.w = pack_weights<Tag>(sc[2 * kb + 1][2], sc[2 * kb + 1][3]);
 #pragma unroll
       for (int db = 0; db < Sh::kDB; ++db) {
-        const uint16_t* vrow = vls + (db * 16 + c16) * Sh::kVP + 4 * g16;
-        const uint2 lo = *reinterpret_cast<const uint2*>(vrow + (2 * kb) * 16);
-        const uint2 hi = *reinterpret_cast<const uint2*>(vrow + (2 * kb + 1) * 16);
+        // tokens 32*kb + 4*g16 + 0..3 (lo) and 16 on (hi) of column db*16 + c16
+        const uint16_t* piece = vls + (kb * 32 + 4 * g16 + c16 / 4) * Sh::kVRP + db * 16 + 4 * (c16 % 4);
+        const uint2 lo = lds_read_col4(piece);
+        const uint2 hi = lds_read_col4(piece + 16 * Sh::kVRP);
         o[db] = Mma<Tag>::run(make_uint4(lo.x, lo.y, hi.x, hi.y), pb, o[db]);
       }
     }
