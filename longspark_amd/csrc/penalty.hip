@@ -36,14 +36,25 @@ __global__ __launch_bounds__(kPTT) void penalty_tables_kernel(
   const int b = blockIdx.x;
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1), wid = tid / kWave;
-  const int n = hist_lens ? min(max(hist_lens[b], 0), hist_cap) : hist_cap;
   const int32_t* h = hist + static_cast<int64_t>(b) * hist_stride;
+  // The first kPre history tokens of each thread are requested before the
+  // table is cleared (their addresses do not depend on the history length).
+  constexpr int kPre = 2;
+  int pre[kPre];
+#pragma unroll
+  for (int u = 0; u < kPre; ++u) pre[u] = tid + u * kPTT < hist_cap ? h[tid + u * kPTT] : -1;
+  const int n = hist_lens ? min(max(hist_lens[b], 0), hist_cap) : hist_cap;
 
   for (int w = tid; w < words; w += kPTT) bits[w] = 0;
   if (freq)
     for (int r = tid; r < hist_cap; r += kPTT) cnt[r] = 0;
   __syncthreads();
-  for (int i = tid; i < n; i += kPTT) {
+#pragma unroll
+  for (int u = 0; u < kPre; ++u) {
+    const int t = pre[u];
+    if (tid + u * kPTT < n && t >= 0 && t < vocab) atomicOr(&bits[t >> 5], 1u << (t & 31));
+  }
+  for (int i = tid + kPre * kPTT; i < n; i += kPTT) {
     const int t = h[i];
     if (t >= 0 && t < vocab) atomicOr(&bits[t >> 5], 1u << (t & 31));
   }
@@ -55,12 +66,7 @@ __global__ __launch_bounds__(kPTT) void penalty_tables_kernel(
   const int w1 = min(words, w0 + per);
   uint32_t c = 0;
   for (int w = w0; w < w1; ++w) c += __popc(bits[w]);
-  uint32_t inc = c;
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) {
-    const uint32_t v = __shfl_up(inc, o, kWave);
-    if (lane >= o) inc += v;
-  }
+  const uint32_t inc = wave_incl_scan_u32(c);
   if (lane == kWave - 1) wave_tot[wid] = inc;
   __syncthreads();
   uint32_t before = 0, distinct = 0;
