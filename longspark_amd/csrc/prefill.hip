@@ -173,8 +173,10 @@ __device__ __forceinline__ void prefill_body(const ls_prefill_args& a, const Pre
   const uint16_t* qrow = qls + min(wave * 16 + c16, tile_rows - 1) * Sh::kKP + g16 * 8;
 
   // Staging assignment: key vector j = i*nthr + tid (token j / kChunks,
-  // chunk j % kChunks); value unit v = i*nthr + tid (tokens 2*(v % (kBlk/2))
-  // and the next, chunk v / (kBlk/2)).  Loads are issued with no branch
+  // chunk j % kChunks); value unit v = i*nthr + tid (tokens 2*(v / kChunks)
+  // and the next, chunk v % kChunks).  Consecutive lanes take consecutive
+  // chunks of a row: whole rows per 16 lanes, in the loads and in the 16-byte
+  // LDS writes (which then fall on distinct banks).  Loads are issued with no branch
   // around them: indices past the step's work are clamped and tokens past
   // the prefix read the last prefix token (those rows get weight 0, so their
   // finite contents are unused).  A load behind a branch makes the compiler
@@ -190,7 +192,7 @@ __device__ __forceinline__ void prefill_body(const ls_prefill_args& a, const Pre
 #pragma unroll
     for (int i = 0; i < Sh::kVR; ++i) {
       const int v = min(i * nthr + tid, Sh::kVUnits - 1);
-      const int p2 = v % (kBlk / 2);
+      const int p2 = v / Sh::kChunks;
 #pragma unroll
       for (int e = 0; e < 2; ++e) L.v[i][e] = table_loc(a, b, min(tb + 2 * p2 + e, t_end - 1));
     }
@@ -204,7 +206,7 @@ __device__ __forceinline__ void prefill_body(const ls_prefill_args& a, const Pre
 #pragma unroll
     for (int i = 0; i < Sh::kVR; ++i) {
       const int v = min(i * nthr + tid, Sh::kVUnits - 1);
-      const int c = v / (kBlk / 2);
+      const int c = v % Sh::kChunks;
 #pragma unroll
       for (int e = 0; e < 2; ++e)
         R.v[i][e] = load16_global(vbase + (static_cast<int64_t>(L.v[i][e]) * a.values.stride_loc + c * 8) * 2);
@@ -221,7 +223,7 @@ __device__ __forceinline__ void prefill_body(const ls_prefill_args& a, const Pre
     for (int i = 0; i < Sh::kVR; ++i) {
       const int v = i * nthr + tid;
       if (v < Sh::kVUnits) {
-        const int p2 = v % (kBlk / 2), c = v / (kBlk / 2);
+        const int p2 = v / Sh::kChunks, c = v % Sh::kChunks;
         *reinterpret_cast<uint4*>(vls + (2 * p2) * Sh::kVRP + c * 8) = R.v[i][0];
         *reinterpret_cast<uint4*>(vls + (2 * p2 + 1) * Sh::kVRP + c * 8) = R.v[i][1];
       }
