@@ -19,7 +19,8 @@
 // Here one workgroup serves (request, KV head): one wave per query head of
 // the group, so each raw key/value row is read from HBM once for all of
 // them (the reference reads it once per query head).  Raw rows are staged in
-// LDS (keys as they are, values transposed to [d][row]); the products run on
+// LDS as they are ([row][d]; the value operand of P.V comes out of a
+// transposing LDS read, ds_read_b64_tr_b16); the products run on
 // v_mfma_f32_16x16x32_bf16 with the 7 query rows padded to 16:
 //   S^T[16 src x 16 rows] = K[16 x 128] . Q^T,   O^T += V^T[16 x 32] . P^T[32 x 16]
 // (the lane holding row c16 gets sources 4*g16 + i of each 16-source tile).
@@ -36,14 +37,14 @@ constexpr int kRaw = 256;        // window rows
 constexpr int kBlk = 64;         // window rows per step (the reference's block)
 constexpr int kChunks = kD / 8;  // 16-byte vectors per row
 constexpr int kKP = kD + 8;      // 16-bit elements per LDS key row
-constexpr int kVP = kBlk + 4;    // 16-bit elements per LDS transposed value row
+constexpr int kVRP = kD + 16;    // 16-bit elements per LDS value row (token-major, skewed as the key rows)
 constexpr int kMinThreads = 256;
 constexpr int kKR = kBlk * kChunks / kMinThreads;         // key vectors per thread per step (4)
 constexpr int kVR = (kBlk / 2) * kChunks / kMinThreads;   // value pairs per thread per step (2)
 constexpr int kKB = kD / 32;
 constexpr int kDB = kD / 16;
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr size_t kLds = static_cast<size_t>(kBlk) * kKP * 2 + static_cast<size_t>(kD) * kVP * 2 + kRaw * 4;
+constexpr size_t kLds = static_cast<size_t>(kBlk) * kKP * 2 + static_cast<size_t>(kBlk) * kVRP * 2 + kRaw * 4;
 
 __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
   typedef __attribute__((ext_vector_type(2))) float f32x2;
@@ -56,10 +57,6 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
 // conversion (v_cvt_pk_bf16_f32) rather than integer rounding with a NaN branch.
 __device__ __forceinline__ float round_bf16(float x) { return __builtin_bit_cast(float, pack_bf16(x, 0.f) << 16); }
 
-__device__ __forceinline__ uint32_t half16(const uint4& v, int e) {
-  const uint32_t w = e < 2 ? v.x : (e < 4 ? v.y : (e < 6 ? v.z : v.w));
-  return (e & 1) ? (w >> 16) : (w & 0xffffu);
-}
 
 // Online-softmax state of the lane's query row (the 4 lanes of a row hold
 // the same m; z is a per-lane partial sum).
@@ -121,7 +118,7 @@ __global__ __launch_bounds__(1024) void draft_attention_kernel(const ls_draft_at
   extern __shared__ __align__(16) char smem[];
   uint16_t* kls = reinterpret_cast<uint16_t*>(smem);
   uint16_t* vls = kls + kBlk * kKP;
-  int32_t* locs = reinterpret_cast<int32_t*>(vls + kD * kVP);  // the request's window rows
+  int32_t* locs = reinterpret_cast<int32_t*>(vls + kBlk * kVRP);  // the request's window rows
 
   const int64_t b = blockIdx.x / a.kv_heads;
   const int kvh = static_cast<int>(blockIdx.x % a.kv_heads);
@@ -175,8 +172,9 @@ __global__ __launch_bounds__(1024) void draft_attention_kernel(const ls_draft_at
     }
 #pragma unroll
     for (int i = 0; i < kVR; ++i) {
+      // chunk-fastest: 16 lanes load (and below write) whole rows
       const int v = min(i * nthr + tid, (kBlk / 2) * kChunks - 1);
-      const int p2 = v % (kBlk / 2), c = v / (kBlk / 2);
+      const int p2 = v / kChunks, c = v % kChunks;
 #pragma unroll
       for (int e = 0; e < 2; ++e) {
         const int64_t loc = locs[min(tb + 2 * p2 + e, raw_len - 1)];
@@ -193,11 +191,9 @@ __global__ __launch_bounds__(1024) void draft_attention_kernel(const ls_draft_at
     for (int i = 0; i < kVR; ++i) {
       const int v = i * nthr + tid;
       if (v < (kBlk / 2) * kChunks) {
-        const int p2 = v % (kBlk / 2), c = v / (kBlk / 2);
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-          *reinterpret_cast<uint32_t*>(vls + (c * 8 + e) * kVP + 2 * p2) =
-              half16(vr[i][0], e) | (half16(vr[i][1], e) << 16);
+        const int p2 = v / kChunks, c = v % kChunks;
+        *reinterpret_cast<uint4*>(vls + (2 * p2) * kVRP + c * 8) = vr[i][0];
+        *reinterpret_cast<uint4*>(vls + (2 * p2 + 1) * kVRP + c * 8) = vr[i][1];
       }
     }
     lds_barrier();
@@ -214,8 +210,9 @@ __global__ __launch_bounds__(1024) void draft_attention_kernel(const ls_draft_at
       for (int i = 0; i < 4; ++i)
         sc[t][i] = tb + t * 16 + 4 * g16 + i < raw_len ? acc[i] * scale2 : -__builtin_inff();
     }
+    // tokens t*16 + 4*g16 + 0..3 of column db*16 + c16, by a transposing read
     fold<kBlk / 16>(st, sc, [&](int db, int t) __attribute__((always_inline)) {
-      return *reinterpret_cast<const uint2*>(vls + (db * 16 + c16) * kVP + t * 16 + 4 * g16);
+      return lds_read_col4(vls + (t * 16 + 4 * g16 + c16 / 4) * kVRP + db * 16 + 4 * (c16 % 4));
     });
   }
   if (!head_wave) return;
