@@ -466,6 +466,8 @@ __global__ __launch_bounds__(kMaxThreads, merge_waves_per_simd<kMaxThreads>()) v
   const uint4 lpb = make_uint4(pack_bf16(lw4[0], lw4[1]), pack_bf16(lw4[2], lw4[3]), 0u, 0u);
   // one reciprocal per normaliser: x * (1/z) is within one fp32 ulp of x / z, far inside the bf16 output
   const float inv_gz = 1.f / gz, inv_lz = 1.f / lz, inv_norm = 1.f / norm;
+  // each source's weight in the merged row, its normaliser folded in
+  const float cr = rw * inv_norm, cg = (inv_gz * gw) * inv_norm, cl = (inv_lz * lw) * inv_norm;
   uint16_t* out = static_cast<uint16_t*>(a.output) + b * a.o_stride_b + head * a.o_stride_h + row * a.o_stride_r;
   // the state rows' LDS writes are counted with the wave's other loads
   if constexpr (kStateLds) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -480,10 +482,14 @@ __global__ __launch_bounds__(kMaxThreads, merge_waves_per_simd<kMaxThreads>()) v
     const f32x4_t lo = Mma<BF16>::run(make_uint4(lvp[db][0], lvp[db][1], 0u, 0u), lpb, zero);
     const uint2 rv = rov[db];
     const float r4[4] = {bf16_lo(rv.x), bf16_hi(rv.x), bf16_lo(rv.y), bf16_hi(rv.y)};
+    // the summary and local sums rounded to bf16 (two per conversion)
+    const uint32_t g01 = pack_bf16(go[0], go[1]), g23 = pack_bf16(go[2], go[3]);
+    const uint32_t l01 = pack_bf16(lo[0], lo[1]), l23 = pack_bf16(lo[2], lo[3]);
+    const float g4r[4] = {bf16_lo(g01), bf16_hi(g01), bf16_lo(g23), bf16_hi(g23)};
+    const float l4r[4] = {bf16_lo(l01), bf16_hi(l01), bf16_lo(l23), bf16_hi(l23)};
     float y[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      y[i] = (r4[i] * rw + (round_bf16(go[i]) * inv_gz) * gw + (round_bf16(lo[i]) * inv_lz) * lw) * inv_norm;
+    for (int i = 0; i < 4; ++i) y[i] = r4[i] * cr + g4r[i] * cg + l4r[i] * cl;
     uint2 w;
     w.x = pack_bf16(y[0], y[1]);
     w.y = pack_bf16(y[2], y[3]);
