@@ -283,7 +283,8 @@ __global__ __launch_bounds__(1024) void draft_attention_kernel(const ls_draft_at
 // Merge form (SRT/speculative/global16_raw256_draft_fused.py:72-312): the
 // window attention arrives as (raw_output, raw_lse); the summary and local
 // sources are normalised on their own and the three merged by their LSEs.
-// One wave per query head; no LDS.
+// One wave per query head; the KV head's local value rows are shared
+// through LDS.
 
 __device__ __forceinline__ float row_max4(float v) { return col4_max(v); }
 __device__ __forceinline__ float row_sum4(float v) { return col4_sum(v); }
@@ -301,6 +302,8 @@ __global__ __launch_bounds__(kMaxThreads, merge_waves_per_simd<kMaxThreads>()) v
     const ls_draft_attention_args a) {
   constexpr bool kStateLds = kMaxThreads <= 256;
   __shared__ float state_lds[kStateLds ? (kMaxThreads / kWave) * kGlobal * kD : 1];
+  constexpr int kLVP = kD + 16;  // 16-bit elements per LDS local value row
+  __shared__ __align__(16) uint16_t local_lds[16 * kLVP];
   const int64_t b = blockIdx.x / a.kv_heads;
   const int kvh = static_cast<int>(blockIdx.x % a.kv_heads);
   const int groups = a.q_heads / a.kv_heads;
@@ -342,23 +345,14 @@ __global__ __launch_bounds__(kMaxThreads, merge_waves_per_simd<kMaxThreads>()) v
       lkb[kb] = load16(lk + kb * 32 + g16 * 8);
     }
   }
-  // local values of sources 4*g16 .. 4*g16+3 (those past the 7 rows are 0), column db*16 + c16, as bf16 pairs
-  uint32_t lvp[kDB][2];
-  {
+  // The 7 local value rows of the KV head are loaded once per workgroup, by
+  // wave 0 (element j of a row by lane j % 64), and written to LDS before the
+  // value products, which read them as the A operand with transposing reads.
+  uint16_t lvh[2 * kLocal];
+  if (wave == 0) {
     const uint16_t* lv = static_cast<const uint16_t*>(a.local_values) + b * a.lv_stride_b + kvh * a.lv_stride_h;
 #pragma unroll
-    for (int db = 0; db < kDB; ++db) {
-      uint32_t h[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        // unconditional load of a clamped row, then a select (no branch per load)
-        const int src = 4 * g16 + e;
-        const uint32_t v = lv[(src < kLocal ? src : kLocal - 1) * a.lv_stride_l + db * 16 + c16];
-        h[e] = src < kLocal ? v : 0u;
-      }
-      lvp[db][0] = h[0] | (h[1] << 16);
-      lvp[db][1] = h[2] | (h[3] << 16);
-    }
+    for (int j = 0; j < 2 * kLocal; ++j) lvh[j] = lv[(j >> 1) * a.lv_stride_l + (j & 1) * kWave + lane];
   }
   bool vis[4];
   {
@@ -469,8 +463,16 @@ __global__ __launch_bounds__(kMaxThreads, merge_waves_per_simd<kMaxThreads>()) v
   // each source's weight in the merged row, its normaliser folded in
   const float cr = rw * inv_norm, cg = (inv_gz * gw) * inv_norm, cl = (inv_lz * lw) * inv_norm;
   uint16_t* out = static_cast<uint16_t*>(a.output) + b * a.o_stride_b + head * a.o_stride_h + row * a.o_stride_r;
+  if (wave == 0) {
+    // local rows 0..6 at pitch kLVP, rows 7..15 zero
+#pragma unroll
+    for (int j = 0; j < 2 * kLocal; ++j) local_lds[(j >> 1) * kLVP + (j & 1) * kWave + lane] = lvh[j];
+#pragma unroll
+    for (int r = kLocal; r < 16; ++r) reinterpret_cast<uint32_t*>(local_lds + r * kLVP)[lane] = 0u;
+  }
   // the state rows' LDS writes are counted with the wave's other loads
   if constexpr (kStateLds) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
 #pragma unroll
   for (int db = 0; db < kDB; ++db) {
     const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
@@ -479,7 +481,9 @@ __global__ __launch_bounds__(kMaxThreads, merge_waves_per_simd<kMaxThreads>()) v
     for (int i = 0; i < 4; ++i)
       g4[i] = kStateLds ? sl[(4 * g16 + i) * kD + ((db * 16 + c16) ^ (16 * g16))] : gvr[kStateLds ? 0 : db][i];
     const f32x4_t go = Mma<BF16>::run(make_uint4(pack_bf16(g4[0], g4[1]), pack_bf16(g4[2], g4[3]), 0u, 0u), gpb, zero);
-    const f32x4_t lo = Mma<BF16>::run(make_uint4(lvp[db][0], lvp[db][1], 0u, 0u), lpb, zero);
+    // local rows 4*g16 + 0..3 (past 6 zero) of column db*16 + c16
+    const uint2 lvr = lds_read_col4(local_lds + (4 * g16 + c16 / 4) * kLVP + db * 16 + 4 * (c16 % 4));
+    const f32x4_t lo = Mma<BF16>::run(make_uint4(lvr.x, lvr.y, 0u, 0u), lpb, zero);
     const uint2 rv = rov[db];
     const float r4[4] = {bf16_lo(rv.x), bf16_hi(rv.x), bf16_lo(rv.y), bf16_hi(rv.y)};
     // the summary and local sums rounded to bf16 (two per conversion)
