@@ -105,6 +105,15 @@ __device__ __forceinline__ uint4 load16(const void* p) {
   return *reinterpret_cast<const uint4*>(p);
 }
 // Streaming read that should not displace reusable lines (logits are read once).
+// A read-only value at a wave-uniform address, loaded through the constant
+// address space: a scalar load, counted apart from the wave's vector loads,
+// so waiting for it never waits for them.  Only for memory that nothing
+// writes while the kernel runs.
+template <typename T>
+__device__ __forceinline__ T load_uniform(const T* p) {
+  return *(const __attribute__((address_space(4))) T*)p;
+}
+
 __device__ __forceinline__ uint4 load16_stream(const void* p) {
   const uint4* q = reinterpret_cast<const uint4*>(p);
   uint4 r;

@@ -1146,15 +1146,20 @@ __device__ __forceinline__ int64_t cand_at(const Args& a, int64_t b, int j) {
   return static_cast<int64_t>(static_cast<const CandT*>(a.cand)[b * a.csb + static_cast<int64_t>(a.cfirst + j) * a.csk]);
 }
 
-__device__ __forceinline__ XForm target_xform(const Args& a, int64_t b, int64_t row) {
+// (rep: the request's repetition penalty, already loaded)
+__device__ __forceinline__ XForm target_xform(const Args& a, int64_t b, int64_t row, float rep) {
   XForm f;
   f.pbits = a.pbits ? a.pbits + b * a.pws : nullptr;
   f.prank = a.pbits ? a.prank + b * a.pws : nullptr;
   f.padd = (a.pbits && a.padd) ? a.padd + b * a.pas : nullptr;
-  f.rep = a.prep ? a.prep[b] : 1.f;
+  f.rep = rep;
   f.quirk = a.quirk;
   f.mbits = a.mask ? a.mask + (a.mask_per_request ? b : row) * a.mrs : nullptr;
   return f;
+}
+
+__device__ __forceinline__ XForm target_xform(const Args& a, int64_t b, int64_t row) {
+  return target_xform(a, b, row, a.prep ? a.prep[b] : 1.f);
 }
 
 // --------------------------------------------------------------- kernels ---
@@ -1448,7 +1453,8 @@ template <typename TagT>
 __device__ __forceinline__ void wave_scan_candidates(WaveShared& ws, const typename TagT::storage* rp, int64_t nelem,
                                                      int64_t e_off, const XForm& f, int k, uint4 (&r)[kWaveDepth],
                                                      uint4 (&q)[kWaveDepth], int& count, float& raw_max, float& kth,
-                                                     int& ovf) {
+                                                     int& ovf, const uint32_t* pre_pw = nullptr,
+                                                     const uint32_t* pre_mw = nullptr) {
   using S = typename TagT::storage;
   constexpr int P = TagT::kPerVec;
   constexpr bool kBf16 = __is_same(TagT, BF16);
@@ -1476,15 +1482,31 @@ __device__ __forceinline__ void wave_scan_candidates(WaveShared& ws, const typen
         pw[u] = 0u;
         mw[u] = ~0u;
       }
-      if (f.pbits) {
+      if (pre_pw) {
+        // the caller loaded the first chunk's words (e_off 0) ahead of the
+        // chunks, word i*64 + l in lane l of pre_*[i]: lane l needs word
+        // ((v*64 + l)*P) >> 5 of its vector v, i.e. register v*P/32, lane
+        // (v*2P) % 64 + (l*P) >> 5
 #pragma unroll
-        for (int u = 0; u < kHalf; ++u)
-          pw[u] = f.pbits[(e_off + static_cast<int64_t>((h * kHalf + u) * kWave + lane) * P) >> 5];
-      }
-      if (f.mbits) {
+        for (int u = 0; u < kHalf; ++u) {
+          constexpr int kRegs = kWaveDepth * 2 * P / kWave;
+          static_assert(kRegs >= 1 && kWave % (2 * P) == 0, "staged word layout");
+          const int v = h * kHalf + u;
+          const int src = (v * 2 * P) % kWave + ((lane * P) >> 5);
+          if (f.pbits) pw[u] = __shfl(pre_pw[(v * P) >> 5], src, kWave);
+          if (f.mbits) mw[u] = __shfl(pre_mw[(v * P) >> 5], src, kWave);
+        }
+      } else {
+        if (f.pbits) {
 #pragma unroll
-        for (int u = 0; u < kHalf; ++u)
-          mw[u] = f.mbits[(e_off + static_cast<int64_t>((h * kHalf + u) * kWave + lane) * P) >> 5];
+          for (int u = 0; u < kHalf; ++u)
+            pw[u] = f.pbits[(e_off + static_cast<int64_t>((h * kHalf + u) * kWave + lane) * P) >> 5];
+        }
+        if (f.mbits) {
+#pragma unroll
+          for (int u = 0; u < kHalf; ++u)
+            mw[u] = f.mbits[(e_off + static_cast<int64_t>((h * kHalf + u) * kWave + lane) * P) >> 5];
+        }
       }
 #pragma unroll
       for (int u = 0; u < kHalf; ++u) {
@@ -2026,6 +2048,8 @@ __device__ __forceinline__ void draft_wave_slice(const Args& a, WaveShared& ws, 
     for (int u = 0; u < kWaveDepth; ++u) r[u] = load16_stream(vp + min<int64_t>(u * kWave + lane, last));
 #pragma unroll
     for (int u = 0; u < kWaveDepth; ++u) q[u] = load16_stream(vp + min<int64_t>((kWaveDepth + u) * kWave + lane, last));
+    // every chunk load is issued before any of them is waited for
+    __builtin_amdgcn_sched_barrier(0);
     wave_scan_candidates<TagD>(ws, rp, nelem, sr.v_begin, f, p.top_k, r, q, count, raw_max, kth, ovf);
     code = (ovf || count > kDraftCap) ? kPubBad : static_cast<uint64_t>(count);
   }
@@ -2178,18 +2202,51 @@ __global__ __launch_bounds__(kWave, 2) void verify_wave_kernel(Args a) {
   const S* rp = static_cast<const S*>(a.logits) + row * a.lrs;
   const uint4* vp = reinterpret_cast<const uint4*>(rp);
   const int64_t last = a.vocab / P - 1;
-  // The first two chunks are requested before the row's parameters are read,
-  // so their latency overlaps the set-up (a row of another path discards them).
+  // The row's parameters are scalar loads, all issued before the first two
+  // chunks are requested: their latency overlaps the chunks', and waiting
+  // for them does not wait for the chunks (a row of another path discards
+  // the chunks).  An absent tensor reads temps[b] in its place.
+  const int j = static_cast<int>(row - b * a.width);
+  const bool has_cand = a.cand && j < a.width - 1;
+  const uint32_t* w_def = reinterpret_cast<const uint32_t*>(a.temps + b);
+  const uint32_t w_temp = load_uniform(w_def);
+  const uint32_t w_k = load_uniform(a.top_ks ? reinterpret_cast<const uint32_t*>(a.top_ks + b) : w_def);
+  const uint32_t w_p = load_uniform(a.top_ps ? reinterpret_cast<const uint32_t*>(a.top_ps + b) : w_def);
+  const uint32_t w_mp = load_uniform(a.min_ps ? reinterpret_cast<const uint32_t*>(a.min_ps + b) : w_def);
+  const uint32_t w_rep = load_uniform(a.prep ? reinterpret_cast<const uint32_t*>(a.prep + b) : w_def);
+  const uint32_t w_np = load_uniform(a.pnonpos ? reinterpret_cast<const uint32_t*>(a.pnonpos + b) : w_def);
+  // (the row's first 16 bytes stand in for an absent drafted token)
+  const CandT w_c = load_uniform(has_cand ? static_cast<const CandT*>(a.cand) + b * a.csb +
+                                                static_cast<int64_t>(a.cfirst + j) * a.csk
+                                          : reinterpret_cast<const CandT*>(rp));
+  // The penalty and mask words of the first chunk's elements (what the
+  // threshold prologue reads) are loaded ahead of the chunks, so the
+  // prologue waits for the first chunk only.
+  constexpr int kPreRegs = kWaveDepth * 2 * P / kWave;  // words of the first chunk / 64
+  const uint32_t* pre_p = a.pbits ? a.pbits + b * a.pws : nullptr;
+  const uint32_t* pre_m = a.mask ? a.mask + (a.mask_per_request ? b : row) * a.mrs : nullptr;
+  // (an absent bitmap reads the row's first bytes in its place: no branch)
+  const uint32_t* pre_pa = pre_p ? pre_p : reinterpret_cast<const uint32_t*>(rp);
+  const uint32_t* pre_ma = pre_m ? pre_m : reinterpret_cast<const uint32_t*>(rp);
+  uint32_t pre_pw[kPreRegs], pre_mw[kPreRegs];
+#pragma unroll
+  for (int i = 0; i < kPreRegs; ++i) {
+    pre_pw[i] = pre_pa[i * kWave + lane];
+    pre_mw[i] = pre_ma[i * kWave + lane];
+  }
+  __builtin_amdgcn_sched_barrier(0);
   uint4 r[kWaveDepth], q[kWaveDepth];
 #pragma unroll
   for (int u = 0; u < kWaveDepth; ++u) r[u] = load16_stream(vp + min<int64_t>(u * kWave + lane, last));
 #pragma unroll
   for (int u = 0; u < kWaveDepth; ++u) q[u] = load16_stream(vp + min<int64_t>((kWaveDepth + u) * kWave + lane, last));
-  Params p{a.temps[b], a.top_ks ? max(a.top_ks[b], 1) : static_cast<int>(a.vocab), a.top_ps ? a.top_ps[b] : 1.f,
-           a.min_ps ? a.min_ps[b] : 0.f};
-  const XForm f = target_xform(a, b, row);
+  // every chunk load is issued before any of them is waited for
+  __builtin_amdgcn_sched_barrier(0);
+  Params p{__uint_as_float(w_temp), a.top_ks ? max(static_cast<int>(w_k), 1) : static_cast<int>(a.vocab),
+           a.top_ps ? __uint_as_float(w_p) : 1.f, a.min_ps ? __uint_as_float(w_mp) : 0.f};
+  const XForm f = target_xform(a, b, row, a.prep ? __uint_as_float(w_rep) : 1.f);
   const int mode = row_mode(p, a.vocab);
-  const bool raw = mode == kModeTopK && raw_filter_ok(f, a.pnonpos, b);
+  const bool raw = mode == kModeTopK && (!f.pbits || (f.rep >= 1.0f && (!f.padd || (a.pnonpos && w_np != 0u))));
   uint64_t word = static_cast<uint64_t>(kFlagOverflow) << 32;  // acceptance not known in this launch
   if (!(raw && p.top_k <= kWaveMaxK)) {
     // Rows of the other paths.  In a raw-only launch the rows that are not raw
@@ -2203,11 +2260,12 @@ __global__ __launch_bounds__(kWave, 2) void verify_wave_kernel(Args a) {
       a.list_t[atomic_add_u32(a.list_cnt, 1u)] = static_cast<int32_t>(row);
     }
   } else {
-    const int cand_tok = cand_tok_of<CandT>(a, row);
+    const int64_t c = static_cast<int64_t>(w_c);
+    const int cand_tok = (has_cand && c >= 0 && c < a.vocab) ? static_cast<int>(c) : -1;
     int count, ovf;
     float raw_max;
     float kth;
-    wave_scan_candidates<TagT>(ws, rp, a.vocab, 0, f, p.top_k, r, q, count, raw_max, kth, ovf);
+    wave_scan_candidates<TagT>(ws, rp, a.vocab, 0, f, p.top_k, r, q, count, raw_max, kth, ovf, pre_pw, pre_mw);
     const RowRec rr = wave_finalize_topk(ws, count, p, raw_max, ovf, a.rec_t + row, a.sidx_t + row * kCap,
                                          a.sp_t + row * kCap, cand_tok, NAN, a.list_cnt, a.list_t,
                                          static_cast<int32_t>(row), true);
