@@ -1833,6 +1833,22 @@ __device__ __forceinline__ Params draft_params(const Args& a, int64_t b) {
   return p;
 }
 
+// The same as scalar loads, all issued at once (an absent tensor reads
+// temps[b] in its place).
+__device__ __forceinline__ Params draft_params_uniform(const Args& a, int64_t b) {
+  const uint32_t* def = reinterpret_cast<const uint32_t*>(a.temps + b);
+  const uint32_t t = load_uniform(a.d_temps ? reinterpret_cast<const uint32_t*>(a.d_temps + b) : def);
+  const uint32_t k = load_uniform(a.d_top_ks ? reinterpret_cast<const uint32_t*>(a.d_top_ks + b) : def);
+  const uint32_t tp = load_uniform(a.d_top_ps ? reinterpret_cast<const uint32_t*>(a.d_top_ps + b) : def);
+  const uint32_t mp = load_uniform(a.d_min_ps ? reinterpret_cast<const uint32_t*>(a.d_min_ps + b) : def);
+  Params p;
+  p.temperature = __uint_as_float(t);
+  p.top_k = a.d_top_ks ? max(static_cast<int>(k), 1) : static_cast<int>(a.vocab);
+  p.top_p = a.d_top_ps ? __uint_as_float(tp) : 1.f;
+  p.min_p = a.d_min_ps ? __uint_as_float(mp) : 0.f;
+  return p;
+}
+
 // First rejected position of request b (width-1 when every drafted token is
 // accepted) and blocking flags, from the target row records.  Called by all
 // 64 lanes of one wave (lane j tests position j); every lane gets the result.
@@ -1949,7 +1965,8 @@ constexpr int kPollLimit = 1 << 19;
 // here (a row up to the rejection went to the exact fallback, or the wait
 // limit passed).  qv / uv: lane j's draft probability and uniform of
 // position j (width <= 64, so one position per lane).
-__device__ __forceinline__ int fused_accept_length(const Args& a, int64_t b, float qv, float uv) {
+// w0: lane k's first read of position k's word (0 past the drafts).
+__device__ __forceinline__ int fused_accept_length(const Args& a, int64_t b, float qv, float uv, uint64_t w0) {
   const int g = a.width - 1;
   const int lane = threadIdx.x & (kWave - 1);
   const uint64_t* acc = a.acc_t + b * a.width;
@@ -1961,7 +1978,7 @@ __device__ __forceinline__ int fused_accept_length(const Args& a, int64_t b, flo
   bool all = true;
   for (int it = 0; it < kPollLimit; ++it) {
     const bool mine = all ? (lane >= j && lane < g) : lane == j;
-    const uint64_t w = mine ? atomic_peek_u64(acc + lane) : 0;
+    const uint64_t w = mine ? (it == 0 ? w0 : atomic_peek_u64(acc + lane)) : 0;
     const bool pub = (w & kAccPublished) != 0;
     const bool ovf = pub && (static_cast<uint32_t>(w >> 32) & kFlagOverflow);
     const bool rej = pub && !ovf && !(uv * qv < __uint_as_float(static_cast<uint32_t>(w)));
@@ -1993,12 +2010,16 @@ __device__ __forceinline__ void draft_wave_slice(const Args& a, WaveShared& ws, 
   constexpr int P = TagD::kPerVec;
   const int lane = threadIdx.x;
   const int g = a.width - 1;
+  // The drafted tokens' probabilities and uniforms, and the first read of
+  // the acceptance words, go out together; the parameters are scalar loads.
   float qv = 0.f, uv = 0.f;
+  uint64_t w0 = 0;
   if (kFused && lane < g) {
+    w0 = atomic_peek_u64(a.acc_t + b * a.width + lane);
     qv = a.dtp[b * a.dtp_sb + lane];
     uv = a.uni[b * a.usb + lane];
   }
-  const Params p = draft_params(a, b);
+  const Params p = kFused ? draft_params_uniform(a, b) : draft_params(a, b);
   const bool topk = row_mode(p, a.vocab) == kModeTopK;
   if (!(topk && p.top_k <= kWaveMaxK)) {
     // A draft row of another path: the workgroup draft scan takes it, or,
@@ -2018,7 +2039,7 @@ __device__ __forceinline__ void draft_wave_slice(const Args& a, WaveShared& ws, 
   const XForm f{nullptr, nullptr, nullptr, 1.f, 0, nullptr};
   int len;
   if constexpr (kFused) {
-    len = fused_accept_length(a, b, qv, uv);
+    len = fused_accept_length(a, b, qv, uv, w0);
   } else {
     int fl;
     len = accept_length_wave<CandT>(a, b, &fl);
