@@ -2674,6 +2674,9 @@ __global__ __launch_bounds__(kT) void resolve_kernel(Args a) {
   const int64_t b = blockIdx.x;
   const int tid = threadIdx.x;
   const int g = a.width - 1;
+  // scalar loads, requested first
+  const Params dpar = draft_params_uniform(a, b);
+  const float u_final = load_uniform(a.funi + b);
   if (tid == 0 && b == 0) {
     atomic_take_u32(a.list_cnt);
     atomic_take_u32(a.list_cnt + 1);
@@ -2711,7 +2714,7 @@ __global__ __launch_bounds__(kT) void resolve_kernel(Args a) {
       }
       int merge = 0;
       if (len < g && a.q_mode == 0 && !fl && !(tr.flags & kFlagOverflow) && a.dwave) {
-        const Params pd = draft_params(a, b);
+        const Params& pd = dpar;
         if (row_mode(pd, a.vocab) == kModeTopK && pd.top_k <= kWaveMaxK) {
           if (__ballot(lane < ns && c >= kPubSkip && c != kPubBad)) {
             // a slice could not decide the acceptance: the exact pass, unscanned
@@ -2749,9 +2752,9 @@ __global__ __launch_bounds__(kT) void resolve_kernel(Args a) {
   RowRec dm{};  // the merged draft record (wave 0)
   const int merge = s_merge;
   if (merge == 1) {
-    dm = draft_merge_block(a, ws, ms, b, draft_params(a, b), s_sbound, s_rawmax, pre);
+    dm = draft_merge_block(a, ws, ms, b, dpar, s_sbound, s_rawmax, pre);
   } else if (merge == 2 && tid < kWave) {
-    dm = wave_finalize_topk(ws, 0, draft_params(a, b), s_rawmax, kWhyMerge, a.rec_d + b, a.sidx_d + b * kCap,
+    dm = wave_finalize_topk(ws, 0, dpar, s_rawmax, kWhyMerge, a.rec_d + b, a.sidx_d + b * kCap,
                             a.sp_d + b * kCap, -1, NAN, a.list_cnt + 1, a.list_d, static_cast<int32_t>(b));
   }
   if (tid < kWave) {
@@ -2783,7 +2786,7 @@ __global__ __launch_bounds__(kT) void resolve_kernel(Args a) {
     }
     return;
   }
-  const float td = a.d_temps ? a.d_temps[b] : a.temps[b];
+  const float td = dpar.temperature;
   // Draft support sorted by index (sparse q rows only) in the upper LDS half.
   uint64_t* dsorted = sh.buf + 2048;
   int dn = 0;
@@ -2791,7 +2794,7 @@ __global__ __launch_bounds__(kT) void resolve_kernel(Args a) {
     dn = dr.n;
     load_sorted_by_index(sh, dsorted, a.sidx_d + b * kCap, a.sp_d + b * kCap, dn);
   }
-  const float u = a.funi[b];
+  const float u = u_final;
   int tok;
   if (tr.n >= 0) {
     // Sparse target support, sorted by index into the lower LDS half.
