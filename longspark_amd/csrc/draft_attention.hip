@@ -130,6 +130,8 @@ __global__ __launch_bounds__(1024) void draft_attention_kernel(const ls_draft_at
   const int head = kvh * groups + (head_wave ? wave : 0);
   const bool row_ok = c16 < kRows;
   const float scale2 = a.softmax_scale * kLog2e;
+  // the request's state slot (a scalar load; used after the window)
+  const int64_t slot = load_uniform(a.state_slots + b);
 
   // Query row c16 of this wave's head as the B operand (rows 7..15 zero).
   uint4 qb[kKB];
@@ -227,7 +229,6 @@ __global__ __launch_bounds__(1024) void draft_attention_kernel(const ls_draft_at
     f32x4_t sc[1];
 #pragma unroll
     for (int i = 0; i < 4; ++i) sc[0][i] = round_bf16(acc[i]) * a.softmax_scale * kLog2e;
-    const int64_t slot = a.state_slots[b];
     const float* gv = a.global_values + slot * a.gv_stride_b + head * a.gv_stride_h;
     fold<1>(st, sc, [&](int db, int) __attribute__((always_inline)) {
       const float* col = gv + (4 * g16) * a.gv_stride_g + db * 16 + c16;
@@ -247,10 +248,13 @@ __global__ __launch_bounds__(1024) void draft_attention_kernel(const ls_draft_at
     }
     f32x4_t sc[1];
     const uint8_t* mrow = a.local_mask + b * a.lm_stride_b + (row_ok ? c16 : 0) * a.lm_stride_r;
+    // the four mask bytes read unconditionally (a clamped index): one round trip
+    uint8_t mb[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) mb[i] = mrow[(4 * g16 + i < kLocal ? 4 * g16 + i : 0) * a.lm_stride_l];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int src = 4 * g16 + i;
-      const bool vis = row_ok && src < kLocal && mrow[(src < kLocal ? src : 0) * a.lm_stride_l] != 0;
+      const bool vis = row_ok && 4 * g16 + i < kLocal && mb[i] != 0;
       sc[0][i] = vis ? round_bf16(acc[i]) * a.softmax_scale * kLog2e : -__builtin_inff();
     }
     const uint16_t* lv = static_cast<const uint16_t*>(a.local_values) + b * a.lv_stride_b + kvh * a.lv_stride_h;
@@ -318,6 +322,9 @@ __global__ __launch_bounds__(kMaxThreads, merge_waves_per_simd<kMaxThreads>()) v
     if (cap > 0.f) s = tanhf(s / cap) * cap;
     return s;
   };
+  // the request's state slot: a scalar load, requested first (the state rows
+  // wait for it, not for the vector loads below)
+  const int64_t slot = load_uniform(a.state_slots + b);
 
   // Every load of the wave is issued here, before any of them is used, so
   // the wave waits for one memory round trip (plus the state slot) instead
@@ -354,20 +361,10 @@ __global__ __launch_bounds__(kMaxThreads, merge_waves_per_simd<kMaxThreads>()) v
 #pragma unroll
     for (int j = 0; j < 2 * kLocal; ++j) lvh[j] = lv[(j >> 1) * a.lv_stride_l + (j & 1) * kWave + lane];
   }
-  bool vis[4];
-  {
-    const uint8_t* mrow = a.local_mask + b * a.lm_stride_b + row * a.lm_stride_r;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int src = 4 * g16 + i;
-      vis[i] = row_ok && src < kLocal && mrow[(src < kLocal ? src : 0) * a.lm_stride_l] != 0;
-    }
-  }
   // summary state rows 4*g16 .. 4*g16+3, column db*16 + c16 (fp32, rounded to bf16 as they are packed)
   float gvr[kStateLds ? 1 : kDB][4];
   float* sl = state_lds + (kStateLds ? wave * kGlobal * kD : 0);
   {
-    const int64_t slot = a.state_slots[b];
     const float* gv = a.global_values + slot * a.gv_stride_b + head * a.gv_stride_h;
     if constexpr (kStateLds) {
       // LDS word r * 128 + (col ^ 16 * (r >> 2)) holds (row r, col): the reads
@@ -387,6 +384,20 @@ __global__ __launch_bounds__(kMaxThreads, merge_waves_per_simd<kMaxThreads>()) v
 #pragma unroll
         for (int i = 0; i < 4; ++i) gvr[db][i] = g[i * a.gv_stride_g + db * 16];
     }
+  }
+  // mask bytes read unconditionally (a clamped index), after the state rows
+  // are requested: a wait for them then waits for no load still to be issued
+  bool vis[4];
+  {
+    const uint8_t* mrow = a.local_mask + b * a.lm_stride_b + row * a.lm_stride_r;
+    uint8_t mb[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int src = 4 * g16 + i;
+      mb[i] = mrow[(src < kLocal ? src : 0) * a.lm_stride_l];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) vis[i] = row_ok && 4 * g16 + i < kLocal && mb[i] != 0;
   }
   if (!row_ok) {
     // q rows past 7 take part in no product's output row, but the tile
