@@ -310,28 +310,52 @@ template <bool kVec>
 __device__ __forceinline__ void chain_chunk(const float* __restrict__ p, const float* __restrict__ q, int64_t vocab,
                                             int64_t c, float* x) {
   const int lane = threadIdx.x & (kWave - 1);
+  if constexpr (kVec) {
+    // All eight 16-byte loads go out unconditionally (a clamped address; q
+    // absent: p again) before any is used; the lanes of a vector that
+    // crosses the end of the row read it element by element.
+    const int64_t vlast = (vocab / 4 - 1) * 4;  // the last whole vector (vocab >= 4)
+    const float* qs = q ? q : p;
+    float4 tp[4], tq[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int64_t v0 = c * kCChunk + i * (kWave * 4) + lane * 4;
-    float pv[4], qv[4] = {0.f, 0.f, 0.f, 0.f};
-    if (kVec && v0 + 3 < vocab) {
-      const float4 t = *reinterpret_cast<const float4*>(p + v0);
-      pv[0] = t.x; pv[1] = t.y; pv[2] = t.z; pv[3] = t.w;
-      if (q) {
-        const float4 d = *reinterpret_cast<const float4*>(q + v0);
-        qv[0] = d.x; qv[1] = d.y; qv[2] = d.z; qv[3] = d.w;
+    for (int i = 0; i < 4; ++i) {
+      const int64_t v0 = c * kCChunk + i * (kWave * 4) + lane * 4;
+      tp[i] = *reinterpret_cast<const float4*>(p + min(v0, vlast));
+      tq[i] = *reinterpret_cast<const float4*>(qs + min(v0, vlast));
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t v0 = c * kCChunk + i * (kWave * 4) + lane * 4;
+      float pv[4] = {tp[i].x, tp[i].y, tp[i].z, tp[i].w};
+      float qv[4] = {tq[i].x, tq[i].y, tq[i].z, tq[i].w};
+      if (v0 + 3 >= vocab) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          pv[e] = v0 + e < vocab ? p[v0 + e] : 0.f;
+          qv[e] = v0 + e < vocab ? qs[v0 + e] : 0.f;
+        }
       }
-    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float d = pv[e] - qv[e];
+        x[4 * i + e] = q ? (d > 0.f ? d : 0.f) : pv[e];
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t v0 = c * kCChunk + i * (kWave * 4) + lane * 4;
+      float pv[4], qv[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         pv[e] = v0 + e < vocab ? p[v0 + e] : 0.f;
         if (q) qv[e] = v0 + e < vocab ? q[v0 + e] : 0.f;
       }
-    }
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float d = pv[e] - qv[e];
-      x[4 * i + e] = q ? (d > 0.f ? d : 0.f) : pv[e];
+      for (int e = 0; e < 4; ++e) {
+        const float d = pv[e] - qv[e];
+        x[4 * i + e] = q ? (d > 0.f ? d : 0.f) : pv[e];
+      }
     }
   }
 }
@@ -622,7 +646,7 @@ extern "C" int ls_chain_speculative_sampling(const ls_chain_sampling_args* args,
   if (slices > a.nchunks) slices = a.nchunks;
   a.cps = static_cast<int>((a.nchunks + slices - 1) / slices);
   a.slices = static_cast<int>((a.nchunks + a.cps - 1) / a.cps);
-  const bool vec = aligned16(x.target_probs) && aligned16(x.draft_probs) && x.tp_stride_b % 4 == 0 &&
+  const bool vec = x.vocab >= 4 && aligned16(x.target_probs) && aligned16(x.draft_probs) && x.tp_stride_b % 4 == 0 &&
                    x.tp_stride_k % 4 == 0 && x.dp_stride_b % 4 == 0 && x.dp_stride_k % 4 == 0;
   const dim3 grid(static_cast<unsigned>(x.batch * a.slices));
   hipStream_t st = static_cast<hipStream_t>(stream);
