@@ -1938,8 +1938,9 @@ __global__ __launch_bounds__(kT) void draft_scan_kernel(Args a) {
 constexpr int kDraftSlices = 32;                  // most slices per request (a.dslices: this launch's)
 // Slices launched per request (at most one per 16 KB chunk of the row):
 // fewer, larger slices leave fewer waves to dispatch after the target rows;
-// of 16, 24 and 32 per fp32 row at V = 151,936, 24 measured fastest.
-constexpr int kDraftSlicesUsed = 24;
+// of 16, 18, 20, 24, 28 and 32 per fp32 row at V = 151,936, 20 measured
+// fastest.
+constexpr int kDraftSlicesUsed = 20;
 constexpr int kDraftMinSlices = 16;               // fewest for the wavefront draft path
 constexpr int kDraftCap = kNBuf / kDraftSlices;  // published candidates per slice (a hand-off row each request)
 
