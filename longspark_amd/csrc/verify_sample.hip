@@ -1474,6 +1474,7 @@ __device__ __forceinline__ void wave_scan_candidates(WaveShared& ws, const typen
     // are fetched 16 vectors at a time.
     float t0 = -INFINITY, t1 = -INFINITY, t2 = -INFINITY, t3 = -INFINITY;
     constexpr int kHalf = 16;
+    static_assert(kWaveDepth % kHalf == 0, "the prologue walks the first chunk in halves of kHalf vectors");
 #pragma unroll
     for (int h = 0; h < kWaveDepth / kHalf; ++h) {
       uint32_t pw[kHalf], mw[kHalf];
@@ -2245,6 +2246,7 @@ __global__ __launch_bounds__(kWave, 2) void verify_wave_kernel(Args a) {
   // threshold prologue reads) are loaded ahead of the chunks, so the
   // prologue waits for the first chunk only.
   constexpr int kPreRegs = kWaveDepth * 2 * P / kWave;  // words of the first chunk / 64
+  static_assert((kWaveDepth * 2 * P) % kWave == 0, "the first chunk's words fill whole registers");
   const uint32_t* pre_p = a.pbits ? a.pbits + b * a.pws : nullptr;
   const uint32_t* pre_m = a.mask ? a.mask + (a.mask_per_request ? b : row) * a.mrs : nullptr;
   // (an absent bitmap reads the row's first bytes in its place: no branch)
